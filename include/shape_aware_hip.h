@@ -1,0 +1,151 @@
+/*
+ * shape_aware_hip.h - C ABI of the MI355X (gfx950) Transformer forward hot path.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and strides (in
+ * elements), scalars and a hipStream_t.  None of them allocates, synchronizes
+ * or throws: work is enqueued asynchronously on `stream` and the return value
+ * is a status code (SAH_OK on success).  sah_last_error() returns a
+ * thread-local description of the most recent failure on the calling thread.
+ *
+ * The reference project binds the equivalent kernels from Python through
+ * torch.library custom ops; the Python side of this project binds these
+ * symbols with ctypes (solution/kernels/hip/_library.py) and registers the same
+ * kind of custom ops around them.
+ */
+#ifndef SHAPE_AWARE_HIP_H_
+#define SHAPE_AWARE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; declared here so the header does not need
+ * the HIP headers (a NULL stream is the legacy default stream). */
+typedef struct ihipStream_t* sah_stream_t;
+
+#define SAH_ABI_VERSION 1
+
+typedef enum {
+  SAH_DTYPE_F32 = 0,
+  SAH_DTYPE_F16 = 1,
+  SAH_DTYPE_BF16 = 2
+} sah_dtype;
+
+typedef enum {
+  SAH_OK = 0,
+  SAH_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, bad stride, bad alignment */
+  SAH_ERR_UNSUPPORTED = 2,      /* shape/dtype/launch outside the implemented kernels */
+  SAH_ERR_HIP = 3,              /* a HIP runtime call or launch failed */
+  SAH_ERR_WORKSPACE = 4         /* workspace missing or too small */
+} sah_status;
+
+typedef enum {
+  SAH_NORM_LAYER = 0, /* y = (x - mean) * rsqrt(var + eps) * weight + bias, biased var */
+  SAH_NORM_RMS = 1    /* y = x * rsqrt(mean(x^2) + eps) * weight (+ bias if given)     */
+} sah_norm_kind;
+
+/* Library identity. */
+int sah_abi_version(void);
+const char* sah_last_error(void);
+
+/*
+ * Causal multi-head attention forward with head_dim 64 and the output written
+ * directly in [B, S, H*64] ("BSD") layout.
+ *
+ * Replaces the reference's
+ *   _streaming_dh64_causal_attention_bsd_op  (solution/shape14/triton_streaming_dh64.py:200-242)
+ *   _streaming_dh64_causal_attention_kernel (solution/shape14/triton_streaming_dh64.py:69-190)
+ * with the same meaning of every argument: query/key/value are [B, H, S, 64]
+ * tensors given by pointer + strides (the packed-QKV view of
+ * solution/operators/projection/qkv_layout.py:22-50 is accepted as is),
+ * `scale` multiplies QK^T before the causal softmax, softmax statistics and
+ * accumulation are fp32, and P is rounded to the input dtype before PV.
+ *
+ * dtype: SAH_DTYPE_BF16 or SAH_DTYPE_F16 for q, k, v and output.
+ * q/k: the head_dim stride must be 1, the seq stride a multiple of 8 and the
+ *      base 16-byte aligned.
+ * v:   either head_dim-contiguous (v_stride_d == 1, the reference layout; the
+ *      kernel then first writes V^T into `workspace`) or seq-contiguous
+ *      (v_stride_s == 1, a V^T buffer; no workspace needed).
+ * out: [B, S, H*64], element stride 1 on the feature axis.
+ * Launch parameters: block_m in {128, 256} query rows per workgroup,
+ *      block_n == 64 keys per tile, num_warps == 4 wavefronts (wave64) per
+ *      workgroup, num_stages in {1, 2} LDS buffers
+ *      (sah_causal_attention_launch_supported() reports the implemented set).
+ */
+int sah_causal_attention_bsd(
+    const void* query, const void* key, const void* value, void* output,
+    int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s, int64_t v_stride_d,
+    int64_t o_stride_b, int64_t o_stride_s,
+    float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages,
+    void* workspace, size_t workspace_bytes,
+    sah_stream_t stream);
+
+/* Workspace bytes sah_causal_attention_bsd needs for this value layout
+ * (0 when value is already seq-contiguous). */
+size_t sah_causal_attention_workspace_bytes(
+    int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+    int64_t v_stride_s, int64_t v_stride_d, int dtype);
+
+/* 1 when (block_m, block_n, num_warps, num_stages) is an implemented launch. */
+int sah_causal_attention_launch_supported(int block_m, int block_n, int num_warps,
+                                          int num_stages);
+
+/*
+ * Fused residual add + LayerNorm / RMSNorm over the last axis:
+ *   residual   = round_to(value_dtype, value + update)
+ *   normalized = round_to(normalized_dtype, norm(residual) * weight + bias)
+ * Statistics are fp32, computed in one pass over HBM (per-lane Welford states
+ * merged across the wavefront).  Both outputs may not alias the inputs.
+ *
+ * Replaces the reference's
+ *   _residual_layer_norm_kernel        (solution/kernels/norm/triton_residual.py:39-71)        fp32 stream
+ *   _mixed_residual_layer_norm_kernel  (solution/kernels/norm/triton_mixed_residual.py:41-76)  fp32 stream + 16-bit update
+ *   residual_add + nn.LayerNorm        (solution/operators/norm/residual_add.py:28-39,
+ *                                       solution/transformer.py:1629-1632)                      same-dtype stream
+ * Implemented dtype combinations (value, update, normalized):
+ *   (bf16,bf16,bf16) (f16,f16,f16) (f32,f32,f32)
+ *   (f32,f16,f16) (f32,f16,f32) (f32,bf16,bf16) (f32,bf16,f32)
+ * weight/bias: param_dtype (f32 or the value dtype); either may be NULL
+ * (weight 1, bias 0).  width: 512 x {1, 2, 4, 8, 16} for 16-bit value dtypes,
+ * 256 x {1, 2, 4, 8, 16} for f32.  Rows are contiguous (row stride == width).
+ * block_rows rows per workgroup of num_warps wavefronts; block_rows must be a
+ * multiple of num_warps; num_warps in {1, 2, 4, 8}.
+ */
+int sah_residual_norm(
+    const void* value, const void* update, const void* weight, const void* bias,
+    void* residual, void* normalized,
+    int64_t rows, int64_t width, float eps,
+    int value_dtype, int update_dtype, int normalized_dtype, int param_dtype,
+    int norm_kind, int block_rows, int num_warps,
+    sah_stream_t stream);
+
+/*
+ * LayerNorm / RMSNorm without a residual (the layer-0 "initial" norm):
+ *   normalized = round_to(normalized_dtype, norm(value) * weight + bias)
+ *
+ * Replaces the reference's
+ *   _initial_fp16_layer_norm_kernel (solution/kernels/norm/triton_initial.py:39-63)
+ *   the TORCH initial norm           (solution/transformer.py:1403-1409)
+ * Implemented (value, normalized): (bf16,bf16) (f16,f16) (f32,f32) (f32,f16) (f32,bf16).
+ * Same width / launch rules as sah_residual_norm.
+ */
+int sah_norm(
+    const void* value, const void* weight, const void* bias, void* normalized,
+    int64_t rows, int64_t width, float eps,
+    int value_dtype, int normalized_dtype, int param_dtype,
+    int norm_kind, int block_rows, int num_warps,
+    sah_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHAPE_AWARE_HIP_H_ */

@@ -1,0 +1,523 @@
+// Causal attention forward, head_dim 64, for gfx950 (CDNA4, wave64, MFMA).
+//
+// Same contract as the reference's streaming kernel
+// (solution/shape14/triton_streaming_dh64.py:69-190): softmax(Q K^T * scale +
+// causal mask) V with an online (running max / running sum) softmax in fp32,
+// P rounded to the input dtype before the PV product, the S x S score matrix
+// never materialized, and the result written straight into [B, S, H*64].
+//
+// MI355X formulation (not a translation of the Triton program):
+//  * Each wavefront owns 32*QG query rows; a workgroup is 4 waves (128*QG rows)
+//    sharing K and V^T tiles of 64 keys staged in LDS (double buffered).
+//  * The score tile is computed transposed, S^T = K Q^T, with
+//    v_mfma_f32_32x32x16_{bf16,f16}: the B operand (Q^T) stays in registers for
+//    the whole kernel and every lane's accumulator column is ONE query row, so
+//    the softmax max and sum are in-lane reductions plus one swap between the
+//    two half-waves.  All 64 lanes' statistics are lane-local, which also makes
+//    the O rescale lane-local.
+//  * K rows are read from LDS in an order with index bits 2 and 3 exchanged.
+//    That makes a lane's S^T registers cover 8 consecutive keys per half-wave,
+//    which is exactly the k-slice the next MFMA needs, so P^T goes from the
+//    score accumulator to the B operand of O^T = V^T P^T without any lane
+//    exchange (one packed fp32->16-bit conversion per pair).
+//  * V^T tiles come from a seq-contiguous V^T buffer (the caller's, or one
+//    written by transpose_v_kernel below), so every LDS read is a 16-byte
+//    ds_read_b128.
+//  * The O rescale by exp(m_old - m_new) is skipped when no row of the wave
+//    raised its maximum (then the factor is exactly 1).
+//  * Grid: one workgroup per (batch*head, query tile).  Workgroup ids are
+//    remapped so that consecutive tiles of the same head land on the same XCD
+//    (the hardware deals ids round-robin over the 8 XCDs), and the longest
+//    (last) query tiles of a head are issued first.
+
+#include <cmath>
+
+#include "sah_common.hpp"
+
+namespace sah {
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kBlockN = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kPad = 8;                   // 16-byte row padding in LDS
+constexpr int kKRow = kHeadDim + kPad;    // K tile row (elements)
+constexpr int kVRow = kBlockN + kPad;     // V^T tile row (elements)
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* vt;  // [B][H][64][>=S], seq stride 1
+  void* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_sd;
+  int64_t o_sb, o_ss;
+  int seq_len;
+  int heads;
+  int num_q_tiles;
+  int num_blocks;
+  float c;  // scale * log2(e)
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float dot2_sum(bf16x2 p, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(p, one, acc, false);
+}
+__device__ __forceinline__ float dot2_sum(f16x2 p, float acc) {
+  const f16x2 one = {(f16)1.0f, (f16)1.0f};
+  return __builtin_amdgcn_fdot2(p, one, acc, false);
+}
+
+// Row of the K tile that MFMA A-row i reads: bits 2 and 3 exchanged.
+__device__ __forceinline__ int k_row_for(int i) {
+  return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+// Load 8 consecutive elements starting at `src` (element index `first` of a
+// row of `limit` valid elements); elements at or past `limit` read as zero.
+template <typename T>
+__device__ __forceinline__ u32x4 load8_guarded(const T* src, int64_t first,
+                                               int64_t limit) {
+  if (first + 8 <= limit) return load16(src);
+  typedef typename Vec8<T>::type V;
+  V v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (first + e < limit) ? src[e] : (T)0.0f;
+  return __builtin_bit_cast(u32x4, v);
+}
+
+template <typename T, int QG, int STAGES>
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
+  typedef typename Vec8<T>::type V8;
+  typedef typename Vec8<T>::half_type V4;
+  typedef typename Vec8<T>::pair_type V2;
+  constexpr int BM = kWaves * 32 * QG;
+
+  __shared__ __attribute__((aligned(16))) T k_lds[STAGES][kBlockN][kKRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[STAGES][kHeadDim][kVRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+
+  // ---- workgroup id -> (batch*head, query tile), XCD-grouped, heavy first.
+  const int bid = blockIdx.x;
+  const int nb = p.num_blocks;
+  const int xcd = bid & 7;
+  const int local = bid >> 3;
+  const int per = nb >> 3;
+  const int rem = nb & 7;
+  const int logical =
+      xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int bh = logical / p.num_q_tiles;
+  const int q_tile = p.num_q_tiles - 1 - (logical - bh * p.num_q_tiles);
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  const int S = p.seq_len;
+
+  const T* qbase = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
+  const T* vbase = static_cast<const T*>(p.vt) + b * p.v_sb + h * p.v_sh;
+  T* obase = static_cast<T*>(p.o) + b * p.o_sb + (int64_t)h * kHeadDim;
+
+  const int q0 = q_tile * BM;
+  const int wq0 = q0 + wave * 32 * QG;                 // first query of this wave
+  // Last valid query of this wave; -1 when the wave has none (skips every tile).
+  const int wq_last = (wq0 < S) ? min(wq0 + 32 * QG, S) - 1 : -1;
+  const int key_end = min(q0 + BM, S);
+  const int n_tiles = (key_end + kBlockN - 1) / kBlockN;
+
+  // ---- Q^T operands (B operand of S^T = K Q^T), kept in registers.
+  V8 qop[QG][4];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    const int qi = wq0 + g * 32 + l32;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
+      qop[g][s] = __builtin_bit_cast(V8, raw);
+    }
+  }
+
+  // ---- cooperative tile loader: 2 x 16 B of K and 2 x 16 B of V^T per thread.
+  u32x4 k_pref[2], v_pref[2];
+  auto load_tile = [&](int tile) {
+    const int k0 = tile * kBlockN;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int row = chunk >> 3;
+      const int c8 = (chunk & 7) * 8;
+      const int key = k0 + row;
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
+      k_pref[i] = raw;
+      // V^T: row = head-dim index, 8 consecutive keys.
+      v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
+                                   (int64_t)k0 + c8, S);
+    }
+  };
+  auto store_tile = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int row = chunk >> 3;
+      const int c8 = (chunk & 7) * 8;
+      *reinterpret_cast<u32x4*>(&k_lds[stage][row][c8]) = k_pref[i];
+      *reinterpret_cast<u32x4*>(&v_lds[stage][row][c8]) = v_pref[i];
+    }
+  };
+
+  // ---- running state (lane-local: query l32 of each group).
+  f32x16 acc[QG][2];
+  float m_run[QG], l_run[QG];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][d][r] = 0.0f;
+  }
+  const float c = p.c;
+  const int a_row = k_row_for(l32);
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const int stage = (STAGES == 2) ? (j & 1) : 0;
+    const bool has_next = j + 1 < n_tiles;
+    if (has_next) load_tile(j + 1);
+    const int k0 = j * kBlockN;
+
+    if (k0 <= wq_last) {  // wave-uniform: skip tiles entirely above this wave's rows
+      // S^T[key][query] for 2 subtiles of 32 keys.
+      f32x16 sacc[QG][2];
+#pragma unroll
+      for (int g = 0; g < QG; ++g)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[g][t][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const V8 a = *reinterpret_cast<const V8*>(
+              &k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
+#pragma unroll
+          for (int g = 0; g < QG; ++g) sacc[g][t] = mfma32(a, qop[g][s], sacc[g][t]);
+        }
+      }
+
+      // Causal mask: only tiles that reach past this wave's first query.
+      if (k0 + kBlockN - 1 > wq0) {
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+          const int qi = wq0 + 32 * g + l32;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = k0 + 32 * t + 16 * (r >> 3) + 8 * half + (r & 7);
+              if (key > qi) sacc[g][t][r] = -INFINITY;
+            }
+        }
+      }
+
+      V8 pb[QG][4];
+#pragma unroll
+      for (int g = 0; g < QG; ++g) {
+        float mx = sacc[g][0][0];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run[g], mx);
+        if (__any(m_new > m_run[g])) {
+          const float alpha = exp2f((m_run[g] - m_new) * c);
+          l_run[g] *= alpha;
+#pragma unroll
+          for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
+          m_run[g] = m_new;
+        }
+        const float mc = m_run[g] * c;
+        float lsum = l_run[g];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int t = u >> 1;
+          const int rb = (u & 1) * 8;
+          V8 pk;
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e], c, -mc));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e + 1], c, -mc));
+            V2 pair;
+            pair[0] = (T)p0;
+            pair[1] = (T)p1;
+            lsum = dot2_sum(pair, lsum);
+            pk[e] = pair[0];
+            pk[e + 1] = pair[1];
+          }
+          pb[g][u] = pk;
+        }
+        l_run[g] = lsum;
+      }
+
+      // O^T[dh][query] += V^T[dh][keys] P^T[keys][query]
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const V8 a = *reinterpret_cast<const V8*>(
+              &v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+#pragma unroll
+          for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(a, pb[g][u], acc[g][d]);
+        }
+      }
+    }
+
+    if (has_next) {
+      if (STAGES == 1) __syncthreads();  // everyone done reading the single buffer
+      store_tile(STAGES == 2 ? ((j + 1) & 1) : 0);
+      __syncthreads();
+    }
+  }
+
+  // ---- normalize and write [B, S, H*64].
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    const int qi = wq0 + 32 * g + l32;
+    const float l_tot = l_run[g] + __shfl_xor(l_run[g], 32);
+    if (qi >= S) continue;
+    const float inv = 1.0f / l_tot;
+    T* orow = obase + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        V4 out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = (T)(acc[g][d][4 * a4 + e] * inv);
+        *reinterpret_cast<V4*>(orow + 32 * d + 8 * a4 + 4 * half) = out;
+      }
+  }
+}
+
+// [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
+// contiguous, zero-filled for keys in [S, S_pad).  One workgroup per 64 keys.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_v_kernel(
+    const T* __restrict__ v, T* __restrict__ vt, int64_t v_sb, int64_t v_sh,
+    int64_t v_ss, int heads, int seq_len, int64_t seq_pad) {
+  __shared__ T tile[64][kHeadDim + 2];
+  const int bh = blockIdx.y;
+  const int b = bh / heads;
+  const int h = bh - b * heads;
+  const int k0 = blockIdx.x * 64;
+  const T* src = v + b * v_sb + h * v_sh;
+  T* dst = vt + (int64_t)bh * kHeadDim * seq_pad;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int chunk = tid + 256 * i;
+    const int row = chunk >> 3;
+    const int c8 = (chunk & 7) * 8;
+    const int key = k0 + row;
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (key < seq_len) raw = load16(src + (int64_t)key * v_ss + c8);
+    typedef typename Vec8<T>::type V8;
+    const V8 vals = __builtin_bit_cast(V8, raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[row][c8 + e] = vals[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int chunk = tid + 256 * i;
+    const int d = chunk >> 3;
+    const int c8 = (chunk & 7) * 8;
+    typedef typename Vec8<T>::type V8;
+    V8 vals;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vals[e] = tile[c8 + e][d];
+    store16(dst + (int64_t)d * seq_pad + k0 + c8, __builtin_bit_cast(u32x4, vals));
+  }
+}
+
+int64_t padded_seq(int64_t seq_len) { return ceil_div(seq_len, 64) * 64; }
+
+bool launch_supported(int block_m, int block_n, int num_warps, int num_stages) {
+  return (block_m == 128 || block_m == 256) && block_n == kBlockN &&
+         num_warps == kWaves && (num_stages == 1 || num_stages == 2);
+}
+
+template <typename T>
+int launch_attention(const AttnParams& prm, int block_m, int num_stages,
+                     hipStream_t stream) {
+  const dim3 grid(prm.num_blocks), block(kThreads);
+  if (block_m == 128) {
+    if (num_stages == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 2>), grid, block, 0, stream, prm);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 1>), grid, block, 0, stream, prm);
+  } else {
+    if (num_stages == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 2>), grid, block, 0, stream, prm);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 1>), grid, block, 0, stream, prm);
+  }
+  return check_hip(hipGetLastError(), "attention kernel launch");
+}
+
+template <typename T>
+int launch_transpose(const void* v, void* vt, int64_t batch, int64_t heads,
+                     int64_t seq_len, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                     hipStream_t stream) {
+  const int64_t seq_pad = padded_seq(seq_len);
+  const dim3 grid((unsigned)(seq_pad / 64), (unsigned)(batch * heads)), block(256);
+  hipLaunchKernelGGL((transpose_v_kernel<T>), grid, block, 0, stream,
+                     static_cast<const T*>(v), static_cast<T*>(vt), v_sb, v_sh, v_ss,
+                     (int)heads, (int)seq_len, seq_pad);
+  return check_hip(hipGetLastError(), "V transpose launch");
+}
+
+}  // namespace
+}  // namespace sah
+
+using namespace sah;
+
+extern "C" int sah_causal_attention_launch_supported(int block_m, int block_n,
+                                                     int num_warps, int num_stages) {
+  return launch_supported(block_m, block_n, num_warps, num_stages) ? 1 : 0;
+}
+
+extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t heads,
+                                                       int64_t seq_len, int64_t head_dim,
+                                                       int64_t v_stride_s,
+                                                       int64_t v_stride_d, int dtype) {
+  (void)head_dim;
+  (void)v_stride_s;
+  if (v_stride_d != 1) return 0;  // already seq-contiguous (V^T storage)
+  const size_t elem = (dtype == SAH_DTYPE_F32) ? 4 : 2;
+  return (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) *
+         elem;
+}
+
+extern "C" int sah_causal_attention_bsd(
+    const void* query, const void* key, const void* value, void* output, int64_t batch,
+    int64_t heads, int64_t seq_len, int64_t head_dim, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages, void* workspace,
+    size_t workspace_bytes, sah_stream_t stream_handle) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+  if (query == nullptr || key == nullptr || value == nullptr || output == nullptr)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "attention tensors must be non-null");
+  if (head_dim != kHeadDim)
+    return fail(SAH_ERR_UNSUPPORTED, "head_dim must be 64 (got %lld)", (long long)head_dim);
+  if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16)
+    return fail(SAH_ERR_UNSUPPORTED, "attention dtype must be bf16 or f16");
+  if (!launch_supported(block_m, block_n, num_warps, num_stages))
+    return fail(SAH_ERR_UNSUPPORTED,
+                "attention launch (block_m=%d, block_n=%d, num_warps=%d, "
+                "num_stages=%d) is not implemented",
+                block_m, block_n, num_warps, num_stages);
+  if (batch < 0 || heads <= 0 || seq_len < 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "invalid attention sizes");
+  if (batch == 0 || seq_len == 0) return SAH_OK;
+  if (seq_len > (int64_t)1 << 30 || batch * heads > (int64_t)1 << 30)
+    return fail(SAH_ERR_UNSUPPORTED, "attention sizes exceed the 32-bit tile indexing");
+  if (!std::isfinite(scale)) return fail(SAH_ERR_INVALID_ARGUMENT, "scale must be finite");
+
+  // Q and K: 16-byte rows.
+  const int64_t qk_strides[] = {q_stride_b, q_stride_h, q_stride_s,
+                                k_stride_b, k_stride_h, k_stride_s};
+  for (int64_t s : qk_strides)
+    if (s % 8 != 0)
+      return fail(SAH_ERR_INVALID_ARGUMENT,
+                  "query/key strides must be multiples of 8 elements");
+  if (!aligned16(query) || !aligned16(key) || !aligned16(output))
+    return fail(SAH_ERR_INVALID_ARGUMENT, "query/key/output must be 16-byte aligned");
+  if (o_stride_b % 4 != 0 || o_stride_s % 4 != 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "output strides must be multiples of 4");
+
+  AttnParams prm;
+  prm.q = query;
+  prm.k = key;
+  prm.o = output;
+  prm.q_sb = q_stride_b;
+  prm.q_sh = q_stride_h;
+  prm.q_ss = q_stride_s;
+  prm.k_sb = k_stride_b;
+  prm.k_sh = k_stride_h;
+  prm.k_ss = k_stride_s;
+  prm.o_sb = o_stride_b;
+  prm.o_ss = o_stride_s;
+  prm.seq_len = (int)seq_len;
+  prm.heads = (int)heads;
+  prm.c = scale * kLog2e;
+  const int64_t q_tiles = ceil_div(seq_len, block_m);
+  const int64_t blocks = q_tiles * batch * heads;
+  if (blocks > INT32_MAX) return fail(SAH_ERR_UNSUPPORTED, "too many attention tiles");
+  prm.num_q_tiles = (int)q_tiles;
+  prm.num_blocks = (int)blocks;
+
+  int status;
+  if (v_stride_d == 1) {
+    // Reference layout: transpose V into the workspace first.
+    const size_t need = sah_causal_attention_workspace_bytes(
+        batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(SAH_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu", need,
+                  workspace_bytes);
+    if (!aligned16(value) || !aligned16(workspace) || v_stride_b % 8 || v_stride_h % 8 ||
+        v_stride_s % 8)
+      return fail(SAH_ERR_INVALID_ARGUMENT,
+                  "value must be 16-byte aligned with strides multiple of 8");
+    status = (dtype == SAH_DTYPE_BF16)
+                 ? launch_transpose<bf16>(value, workspace, batch, heads, seq_len,
+                                          v_stride_b, v_stride_h, v_stride_s, stream)
+                 : launch_transpose<f16>(value, workspace, batch, heads, seq_len,
+                                         v_stride_b, v_stride_h, v_stride_s, stream);
+    if (status != SAH_OK) return status;
+    const int64_t seq_pad = padded_seq(seq_len);
+    prm.vt = workspace;
+    prm.v_sb = heads * kHeadDim * seq_pad;
+    prm.v_sh = kHeadDim * seq_pad;
+    prm.v_sd = seq_pad;
+  } else if (v_stride_s == 1) {
+    if (!aligned16(value) || v_stride_b % 8 || v_stride_h % 8 || v_stride_d % 8)
+      return fail(SAH_ERR_INVALID_ARGUMENT,
+                  "seq-contiguous value must be 16-byte aligned with strides multiple of 8");
+    prm.vt = value;
+    prm.v_sb = v_stride_b;
+    prm.v_sh = v_stride_h;
+    prm.v_sd = v_stride_d;
+  } else {
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "value needs a unit stride on the head_dim or the seq axis");
+  }
+  return (dtype == SAH_DTYPE_BF16) ? launch_attention<bf16>(prm, block_m, num_stages, stream)
+                                   : launch_attention<f16>(prm, block_m, num_stages, stream);
+}

@@ -1,0 +1,151 @@
+"""Build libshape_aware_hip.so for gfx950 from the HIP sources in this folder.
+
+The device code is compiled by the system hipcc (ROCm 7.2, ``--offload-arch=
+gfx950``) and the shared library is linked against the HIP runtime that ships
+inside the installed PyTorch wheel, so one process holds exactly one HIP
+runtime (the one torch's streams and allocations live in).  Every HIP symbol
+the library imports is checked against that runtime's export table.
+
+Usage:  python build.py [--verbose]
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PACKAGE_ROOT = CSRC.parent
+LIB_DIR = PACKAGE_ROOT / "lib"
+BUILD_DIR = CSRC / "_build"
+LIBRARY_NAME = "libshape_aware_hip.so"
+SOURCES = ("capi.hip", "residual_norm.hip", "attention_fwd.hip")
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = (
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    # Keep the compiler from forming packed-FP32 VALU instructions.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
+
+
+def _torch_lib_dir() -> Path:
+    import importlib.util
+
+    spec = importlib.util.find_spec("torch")
+    if spec is None or spec.origin is None:
+        raise RuntimeError("PyTorch is required to locate its HIP runtime")
+    lib = Path(spec.origin).resolve().parent / "lib"
+    if not (lib / "libamdhip64.so").exists():
+        raise RuntimeError(f"no libamdhip64.so in {lib}; a ROCm build of torch is required")
+    return lib
+
+
+def _hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    completed = subprocess.run(cmd, capture_output=True, text=True, check=False)
+    noise = "is not a recognized feature for this target"
+    stderr = "\n".join(line for line in completed.stderr.splitlines() if noise not in line)
+    if completed.returncode != 0:
+        raise RuntimeError(f"command failed ({completed.returncode}): {' '.join(cmd)}\n{stderr}")
+    if verbose and stderr.strip():
+        print(stderr, flush=True)
+
+
+def _dynamic_symbols(path: Path, *, defined: bool) -> set[str]:
+    flag = "--defined-only" if defined else "--undefined-only"
+    out = subprocess.run(
+        ["nm", "-D", flag, str(path)], capture_output=True, text=True, check=True
+    ).stdout
+    names = set()
+    for line in out.splitlines():
+        parts = line.split()
+        if not parts:
+            continue
+        names.add(parts[-1].split("@")[0])
+    return names
+
+
+def _check_runtime_symbols(library: Path, torch_lib: Path) -> None:
+    wanted = {
+        name
+        for name in _dynamic_symbols(library, defined=False)
+        if name.startswith(("hip", "__hip"))
+    }
+    exported = _dynamic_symbols(torch_lib / "libamdhip64.so", defined=True)
+    missing = sorted(wanted - exported)
+    if missing:
+        raise RuntimeError(
+            "the library imports HIP symbols torch's runtime does not export: "
+            + ", ".join(missing)
+        )
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link the shared library; return its path."""
+
+    hipcc = _hipcc()
+    torch_lib = _torch_lib_dir()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+
+    def compile_one(source: str) -> Path:
+        obj = BUILD_DIR / (Path(source).stem + ".o")
+        _run([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / source), "-o", str(obj)], verbose)
+        return obj
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        objects = list(pool.map(compile_one, SOURCES))
+
+    tmp = LIB_DIR / (LIBRARY_NAME + ".tmp")
+    _run(
+        [
+            "g++",
+            "-shared",
+            "-o",
+            str(tmp),
+            *map(str, objects),
+            f"-L{torch_lib}",
+            "-l:libamdhip64.so",
+            f"-Wl,-rpath,{torch_lib}",
+            "-Wl,--no-undefined",
+        ],
+        verbose,
+    )
+    _check_runtime_symbols(tmp, torch_lib)
+    target = LIB_DIR / LIBRARY_NAME
+    os.replace(tmp, target)
+    return target
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--verbose", action="store_true")
+    args = parser.parse_args()
+    path = build(verbose=args.verbose)
+    print(path)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

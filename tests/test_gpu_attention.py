@@ -1,0 +1,197 @@
+"""GPU parity of the gfx950 causal attention kernel against the CPU oracle.
+
+Gate (written here, applied elementwise like the official OR rule): a bf16 or
+fp16 output element passes when |err| <= 2e-2 or |err| <= 1e-2 * |ref|, with
+the reference computed in fp32 (float64 for the sampled long-sequence rows)
+from the same 16-bit inputs.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.compare import parity_gate
+from oracle.forward import causal_attention_rows, query_block_causal_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _attention_module():
+    from solution.shape14 import hip_streaming_dh64
+
+    return hip_streaming_dh64
+
+
+def _inputs(batch, heads, seq, *, dtype, seed, scale_inputs=1.0):
+    generator = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq, 64)
+    q, k, v = (torch.randn(shape, generator=generator) * scale_inputs for _ in range(3))
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def _oracle(q, k, v, scale):
+    return query_block_causal_attention(q.float(), k.float(), v.float(), scale)
+
+
+def _to_bsd(context_bhsd: torch.Tensor) -> torch.Tensor:
+    batch, heads, seq, dim = context_bhsd.shape
+    return context_bhsd.transpose(1, 2).reshape(batch, seq, heads * dim)
+
+
+def _run(q, k, v, device, **launch):
+    module = _attention_module()
+    with torch.inference_mode():
+        output, marker = module.hip_streaming_dh64_causal_attention_bsd(
+            q.to(device), k.to(device), v.to(device), scale=1 / 8, **launch
+        )
+    assert marker == module.HIP_STREAMING_DH64_CAUSAL_ATTENTION_BSD_BACKEND
+    torch.cuda.synchronize(device)
+    return output
+
+
+def _assert_parity(reference, candidate, dtype, what):
+    result = parity_gate(reference, candidate.float().cpu(), dtype)
+    assert result.passed, (
+        f"{what}: {result.failed_elements}/{result.total_elements} failed, "
+        f"max_abs={result.max_abs_error:.4g} at {result.worst_index}"
+    )
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_m", [128, 256])
+@pytest.mark.parametrize(
+    "batch,heads,seq",
+    [(1, 1, 1), (1, 2, 17), (2, 3, 100), (2, 2, 257), (1, 2, 1000), (3, 1, 130)],
+)
+def test_attention_matches_oracle(gpu_device, dtype, block_m, batch, heads, seq):
+    print(f"attention parity dtype={dtype} block_m={block_m} shape={(batch, heads, seq)}", flush=True)
+    q, k, v = _inputs(batch, heads, seq, dtype=dtype, seed=seq * 7 + heads)
+    output = _run(q, k, v, gpu_device, block_m=block_m)
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    _assert_parity(reference, output, dtype, f"{dtype} {block_m} {(batch, heads, seq)}")
+
+
+@pytest.mark.parametrize("num_stages", [1, 2])
+def test_baseline_config3_attention(gpu_device, num_stages):
+    """B8 H16 S2048 Dh64, inputs N(0,1)/sqrt(64); the op
+    applies the 1/sqrt(64) softmax scale on top."""
+
+    print(f"config-3 attention num_stages={num_stages}", flush=True)
+    q, k, v = _inputs(8, 16, 2048, dtype=torch.bfloat16, seed=1234, scale_inputs=1 / 8)
+    output = _run(q, k, v, gpu_device, block_m=128, num_stages=num_stages)
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    _assert_parity(reference, output, torch.bfloat16, "config 3")
+
+
+def test_launch_shapes_and_stages_are_bitwise_identical(gpu_device):
+    """The result of a query row does not depend on the tiling of the grid."""
+
+    q, k, v = _inputs(2, 4, 777, dtype=torch.bfloat16, seed=5)
+    outputs = [
+        _run(q, k, v, gpu_device, block_m=block_m, num_stages=stages)
+        for block_m in (128, 256)
+        for stages in (1, 2)
+    ]
+    for other in outputs[1:]:
+        assert torch.equal(outputs[0], other)
+
+
+def test_packed_qkv_view_and_transposed_value_layouts_agree(gpu_device):
+    """The reference's zero-copy split of [B,S,3D] (strided, head_dim
+    contiguous V) and a seq-contiguous V^T buffer give identical results."""
+
+    batch, seq, heads = 2, 300, 4
+    width = heads * 64
+    generator = torch.Generator().manual_seed(11)
+    packed = torch.randn(batch, seq, 3 * width, generator=generator).to(torch.bfloat16)
+    packed_gpu = packed.to(gpu_device)
+    q, k, v = (
+        t.transpose(1, 2) for t in packed_gpu.unflatten(-1, (3, heads, 64)).unbind(dim=2)
+    )
+    assert q.stride(-1) == 1 and not q.is_contiguous()
+    module = _attention_module()
+    with torch.inference_mode():
+        from_view, _ = module.hip_streaming_dh64_causal_attention_bsd(q, k, v, scale=1 / 8)
+        seq_pad = 320
+        v_t = torch.zeros(batch, heads, 64, seq_pad, dtype=torch.bfloat16, device=gpu_device)
+        v_t[..., :seq] = v.transpose(-1, -2)
+        v_seq_major = v_t[..., :seq].transpose(-1, -2)
+        assert v_seq_major.stride(-2) == 1
+        from_vt, _ = module.hip_streaming_dh64_causal_attention_bsd(q, k, v_seq_major, scale=1 / 8)
+    assert torch.equal(from_view, from_vt)
+    reference = _to_bsd(_oracle(q.cpu(), k.cpu(), v.cpu(), 1 / 8))
+    _assert_parity(reference, from_view, torch.bfloat16, "packed view")
+
+
+def test_constant_value_rows_are_reproduced(gpu_device):
+    """Softmax weights sum to one, so a constant V column yields that constant."""
+
+    q, k, _ = _inputs(1, 2, 513, dtype=torch.bfloat16, seed=3)
+    columns = torch.linspace(-3, 3, 64).to(torch.bfloat16)
+    v = columns.expand(1, 2, 513, 64).contiguous()
+    output = _run(q, k, v, gpu_device).float().cpu()
+    expected = columns.float().repeat(2).expand(1, 513, 128)
+    assert (output - expected).abs().max().item() <= 2e-2
+
+
+def test_zero_query_gives_running_prefix_mean(gpu_device):
+    """Q = 0 makes every visible key equally likely: row i is mean(V[0..i])."""
+
+    _, k, v = _inputs(1, 1, 300, dtype=torch.bfloat16, seed=9)
+    q = torch.zeros_like(k)
+    output = _run(q, k, v, gpu_device).float().cpu()[0]
+    prefix = torch.cumsum(v[0, 0].double(), dim=0) / torch.arange(1, 301).double()[:, None]
+    _assert_parity(prefix.float(), output, torch.bfloat16, "prefix mean")
+
+
+def test_first_row_copies_first_value(gpu_device):
+    q, k, v = _inputs(2, 3, 64, dtype=torch.bfloat16, seed=21)
+    output = _run(q, k, v, gpu_device).cpu()
+    for head in range(3):
+        assert torch.equal(output[:, 0, head * 64 : (head + 1) * 64], v[:, head, 0])
+
+
+def test_batch_slices_are_independent(gpu_device):
+    """Running a sub-batch gives bitwise the rows of the full batch (the
+    property the streamed chunk driver relies on)."""
+
+    q, k, v = _inputs(4, 2, 400, dtype=torch.bfloat16, seed=17)
+    full = _run(q, k, v, gpu_device)
+    part = _run(q[1:3], k[1:3], v[1:3], gpu_device)
+    assert torch.equal(full[1:3], part)
+
+
+def test_long_sequence_sampled_rows(gpu_device):
+    """S = 100000 (the long-sequence configuration's length): sampled rows,
+    including the last ones that see every key, against float64 per-row math."""
+
+    seq = 100_000
+    print("long-sequence attention S=100000", flush=True)
+    q, k, v = _inputs(1, 2, seq, dtype=torch.bfloat16, seed=2024)
+    output = _run(q, k, v, gpu_device, block_m=256).float().cpu()
+    rng = np.random.default_rng(0)
+    rows = np.unique(
+        np.concatenate([np.arange(0, 40), np.arange(seq - 40, seq), rng.integers(0, seq, 40)])
+    )
+    for head in range(2):
+        expected = causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(),
+            rows, 1 / 8,
+        )
+        actual = output[0, rows, head * 64 : (head + 1) * 64]
+        _assert_parity(torch.from_numpy(expected).float(), actual, torch.bfloat16, f"head {head}")
+
+
+def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
+    module = _attention_module()
+    q, k, v = (t.to(gpu_device) for t in _inputs(1, 1, 64, dtype=torch.bfloat16, seed=1))
+    with torch.inference_mode():
+        with pytest.raises(ValueError):
+            module.prevalidated_hip_streaming_dh64_causal_attention_bsd(q, k, v, block_m=64)
+        with pytest.raises(RuntimeError, match="ineligible"):
+            module.hip_streaming_dh64_causal_attention_bsd(q.float(), k.float(), v.float())
+    assert not module.can_use_hip_streaming_dh64_causal_attention(q, k, v, causal=False)
