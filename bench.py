@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the Transformer forward hot path on one MI355X.
+
+Workload (BASELINE.json's metric configuration, "configs[4]"): a 2-layer
+pre-LN causal Transformer, B=32 S=100000 D=1024 H=16 (head_dim 64) FFN 4096,
+bf16, seeded Xavier-uniform weights (zero biases, LayerNorm 1/0) and N(0,1)
+inputs, executed by the plugin model's streamed HIP program as 16 ordered
+B=2 chunks.  One "step" is one full B=32 forward; inputs are resident in HBM
+before the timed region.
+
+Printed on stdout: ONE JSON line.  ``value`` is the forward latency in ms
+(lower is better).  ``roofline`` covers the dominant kernel, the causal
+attention: achieved TFLOP/s = algorithmic FLOPs (4*B*H*Dh*S(S+1)/2 per
+launch) / the launches' mean duration, timed with HIP events recorded on the
+launch stream around every attention launch inside the timed region.
+``cpu_baseline`` times the CPU oracle (fp32 official order, query-blocked
+attention) on a bounded sample of the same workload and scales it to one
+full forward.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PACKAGE_DIR = ROOT / "ml-guided-program-search-for-shape-specialized-transformer-optimization_amd"
+for _path in (PACKAGE_DIR, ROOT):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+METRIC = "fwd latency ms + attn TFLOP/s (% MFMA peak), B=32 S=100k D=1024 H=16 causal"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+WORKLOAD = dict(batch=32, seq_len=100_000, d_model=1024, heads=16, ffn_dim=4096, layers=2, microbatch=2)
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+class _Config:
+    def __init__(self, batch, seq_len, d_model, heads, ffn_dim, layers):
+        self.batch_size = batch
+        self.seq_len = seq_len
+        self.d_model = d_model
+        self.num_heads = heads
+        self.ffn_dim = ffn_dim
+        self.num_layers = layers
+        self.causal = True
+
+
+def _init_xavier(model, seed: int) -> None:
+    """Seeded Xavier-uniform for every projection role (q, k and v separately
+    inside the packed qkv_proj), zero biases, LayerNorm weight 1 / bias 0."""
+
+    import torch
+
+    generator = torch.Generator().manual_seed(seed)
+
+    def fill(weight):
+        out_features, in_features = weight.shape
+        bound = math.sqrt(6.0 / (in_features + out_features))
+        return (torch.rand(out_features, in_features, generator=generator) * 2 - 1) * bound
+
+    with torch.no_grad():
+        for layer in model.layers:
+            d = layer.attention.d_model
+            packed = layer.attention.qkv_proj.weight
+            for index in range(3):
+                packed[index * d : (index + 1) * d].copy_(fill(packed[index * d : (index + 1) * d]))
+            for linear in (layer.attention.out_proj, layer.ffn_in, layer.ffn_out):
+                linear.weight.copy_(fill(linear.weight))
+            for linear in (layer.attention.qkv_proj, layer.attention.out_proj, layer.ffn_in, layer.ffn_out):
+                linear.bias.zero_()
+        for module in model.modules():
+            if isinstance(module, torch.nn.LayerNorm):
+                module.weight.fill_(1.0)
+                module.bias.zero_()
+
+
+class _KernelTimer:
+    """Wraps a launcher so every call is bracketed by HIP events on the
+    current (launch) stream; durations are read after the timed region."""
+
+    def __init__(self, module, name: str):
+        self.module = module
+        self.name = name
+        self.original = getattr(module, name)
+        self.events = []
+        self.work = []
+        self.active = False
+
+    def install(self, work_of):
+        import torch
+
+        def wrapped(*args, **kwargs):
+            if not self.active:
+                return self.original(*args, **kwargs)
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            result = self.original(*args, **kwargs)
+            end.record()
+            self.events.append((start, end))
+            self.work.append(work_of(*args, **kwargs))
+            return result
+
+        setattr(self.module, self.name, wrapped)
+
+    def summary(self):
+        durations = [start.elapsed_time(end) for start, end in self.events]
+        return durations, self.work
+
+
+def _attention_flops(query, *args, **kwargs) -> float:
+    batch, heads, seq, dim = query.shape
+    return 4.0 * batch * heads * dim * (seq * (seq + 1) // 2)
+
+
+def _norm_bytes(value, update, weight, bias, eps, normalized_dtype, *args, **kwargs) -> float:
+    import torch
+
+    width = value.shape[-1]
+    rows = value.numel() // width
+    out_size = torch.empty((), dtype=normalized_dtype).element_size()
+    per = 2 * value.element_size() + update.element_size() + out_size
+    params = sum(t.numel() * t.element_size() for t in (weight, bias) if t is not None)
+    return float(rows * width * per + params)
+
+
+def gpu_benchmark(steps: int, warmup: int) -> dict:
+    import torch
+
+    from solution.config import hip_config
+    from solution.kernels.hip import load_library
+    from solution.kernels.norm import hip_residual
+    from solution.shape14 import hip_streaming_dh64
+    from solution.transformer import UserOptimizedTransformer
+
+    load_library()
+    device = torch.device("cuda", 0)
+    w = WORKLOAD
+    config = _Config(w["batch"], w["seq_len"], w["d_model"], w["heads"], w["ffn_dim"], w["layers"])
+    model = UserOptimizedTransformer(config)
+    _init_xavier(model, seed=1234)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    program = hip_config(microbatch_size=w["microbatch"])
+    model.configure_execution(config=program)
+
+    generator = torch.Generator(device=device).manual_seed(1234)
+    x = torch.randn(w["batch"], w["seq_len"], w["d_model"], generator=generator, device=device,
+                    dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    log(f"input resident: {tuple(x.shape)} bf16, program {program.config_id}")
+
+    attention_timer = _KernelTimer(hip_streaming_dh64, "_launch")
+    attention_timer.install(_attention_flops)
+    norm_timer = _KernelTimer(hip_residual, "_launch_residual")
+    norm_timer.install(_norm_bytes)
+
+    with torch.inference_mode():
+        # Peak HBM of one B=2 chunk (same program, one microbatch).
+        chunk = x[: w["microbatch"]].contiguous()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(device)
+        before = torch.cuda.memory_allocated(device)
+        model(chunk)
+        torch.cuda.synchronize()
+        peak_chunk = torch.cuda.max_memory_allocated(device) - before
+        del chunk
+        log(f"peak HBM above resident tensors for one B=2 chunk: {peak_chunk / 2**30:.2f} GiB")
+
+        for index in range(warmup):
+            model(x)
+            torch.cuda.synchronize()
+            log(f"warmup step {index + 1}/{warmup} done")
+
+        attention_timer.active = True
+        norm_timer.active = True
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for index in range(steps):
+            output = model(x)
+            log(f"timed step {index + 1}/{steps} issued")
+        end.record()
+        torch.cuda.synchronize()
+        attention_timer.active = False
+        norm_timer.active = False
+        total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / steps
+    assert torch.isfinite(output[:, :: 997]).all(), "non-finite output"
+
+    durations, flops = attention_timer.summary()
+    attention_ms = sum(durations) / len(durations)
+    attention_flops = sum(flops) / len(flops)
+    attention_tflops = attention_flops / (attention_ms * 1e-3) / 1e12
+    norm_durations, norm_work = norm_timer.summary()
+    norm_us = 1e3 * sum(norm_durations) / len(norm_durations)
+    norm_gbs = (sum(norm_work) / len(norm_work)) / (norm_us * 1e-6) / 1e9
+
+    layers, batch, seq, width, ffn = w["layers"], w["batch"], w["seq_len"], w["d_model"], w["ffn_dim"]
+    model_flops = layers * (2 * batch * seq * seq * width + 8 * batch * seq * width**2 + 4 * batch * seq * width * ffn)
+    log(f"{ms_per_step:.1f} ms/step; attention {attention_ms:.3f} ms/launch {attention_tflops:.1f} TFLOP/s; "
+        f"norm {norm_us:.1f} us/launch {norm_gbs:.0f} GB/s")
+    return {
+        "ms_per_step": ms_per_step,
+        "attention_ms_per_launch": attention_ms,
+        "attention_launches_per_step": len(durations) // steps,
+        "attention_flops_per_launch": attention_flops,
+        "attention_tflops": attention_tflops,
+        "attention_share_of_step": sum(durations) / total_ms,
+        "norm_us_per_launch": norm_us,
+        "norm_bytes_per_launch": sum(norm_work) / len(norm_work),
+        "norm_gbs": norm_gbs,
+        "peak_hbm_bytes_per_chunk": int(peak_chunk),
+        "model_flops": model_flops,
+        "config_id": program.config_id,
+    }
+
+
+def cpu_baseline() -> dict:
+    """Time the CPU oracle on a bounded sample and scale to one full forward.
+
+    The oracle's fp32 official-order forward (oracle.forward, query-blocked
+    attention: every 128-row block scores all keys, as the reference's
+    portable path does) runs one layer of one sequence of the workload's
+    widths at three lengths S_i.  A least-squares fit t(S) = a*S + b*S^2
+    (row-wise work is linear in S, query-blocked attention quadratic)
+    extrapolates to S = 100000, then x layers x sequences.
+    """
+
+    import numpy as np
+    import torch
+
+    from oracle.forward import TransformerConfig, forward, generate_input, xavier_init_weights
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(threads)
+    w = WORKLOAD
+    lengths = (2048, 4096, 8192)
+    times = []
+    with torch.inference_mode():
+        for seq in lengths:
+            config = TransformerConfig(1, seq, w["d_model"], w["heads"], w["ffn_dim"], 1, True)
+            state = xavier_init_weights(config, seed=1234)
+            x = generate_input(config, seed=1234)
+            forward(state, x[:, :256], TransformerConfig(1, 256, w["d_model"], w["heads"], w["ffn_dim"], 1, True))
+            t0 = time.perf_counter()
+            forward(state, x, config, attention="query_block")
+            times.append(time.perf_counter() - t0)
+    design = np.array([[s, s * s] for s in lengths], dtype=np.float64)
+    (a, b), *_ = np.linalg.lstsq(design, np.array(times), rcond=None)
+    seq = w["seq_len"]
+    per_layer_per_sequence = a * seq + b * seq * seq
+    full_ms = per_layer_per_sequence * w["layers"] * w["batch"] * 1e3
+    return {
+        "value": round(full_ms, 1),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            "fp32 oracle forward (official op order, query-blocked attention), one layer of one "
+            f"sequence at D1024 H16 F4096 for S in {list(lengths)} "
+            f"({', '.join(f'{t:.2f}' for t in times)} s); t(S)=a*S+b*S^2 least-squares fit "
+            f"extrapolated to S={seq}, x {w['layers']} layers x {w['batch']} sequences"
+        ),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU only: the long-sequence workload is "
+            "data-parallel over independent sequences, so N GPUs would each run "
+            "batch/N sequences with no exchange (see the sharding note in DESIGN.md).",
+            file=sys.stderr,
+        )
+        return 2
+    if args.steps <= 0 or args.warmup < 0:
+        raise SystemExit("--steps must be positive and --warmup non-negative")
+
+    gpu = gpu_benchmark(args.steps, args.warmup)
+    baseline = None if args.no_cpu_baseline else cpu_baseline()
+    if baseline is not None:
+        log(f"cpu baseline: {baseline['value'] / 1e3:.0f} s per forward on {baseline['cores']} threads")
+    achieved = gpu["attention_tflops"]
+    record = {
+        "metric": METRIC,
+        "value": round(gpu["ms_per_step"], 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_per_step"], 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "long-sequence streamed forward (BASELINE configs[4])",
+            "batch": WORKLOAD["batch"],
+            "seq_len": WORKLOAD["seq_len"],
+            "d_model": WORKLOAD["d_model"],
+            "heads": WORKLOAD["heads"],
+            "head_dim": WORKLOAD["d_model"] // WORKLOAD["heads"],
+            "ffn_dim": WORKLOAD["ffn_dim"],
+            "layers": WORKLOAD["layers"],
+            "microbatch": WORKLOAD["microbatch"],
+            "chunks": WORKLOAD["batch"] // WORKLOAD["microbatch"],
+            "config_id": gpu["config_id"],
+        },
+        "attention": {
+            "tflops": round(achieved, 1),
+            "pct_mfma_peak": round(100 * achieved / PEAK_BF16_TFLOPS, 2),
+            "ms_per_launch": round(gpu["attention_ms_per_launch"], 3),
+            "launches_per_step": gpu["attention_launches_per_step"],
+            "share_of_step": round(gpu["attention_share_of_step"], 4),
+        },
+        "norm": {
+            "gbs": round(gpu["norm_gbs"], 1),
+            "pct_hbm_peak": round(100 * gpu["norm_gbs"] / PEAK_HBM_GBS, 2),
+            "us_per_launch": round(gpu["norm_us_per_launch"], 2),
+            "bytes_per_launch": int(gpu["norm_bytes_per_launch"]),
+        },
+        "model_tflops": round(gpu["model_flops"] / (gpu["ms_per_step"] * 1e-3) / 1e12, 1),
+        "peak_hbm_bytes_per_chunk": gpu["peak_hbm_bytes_per_chunk"],
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

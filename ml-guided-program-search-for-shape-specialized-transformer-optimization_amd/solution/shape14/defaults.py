@@ -1,0 +1,65 @@
+"""Default streamed programs.
+
+conservative_streamed_config restates the reference's measured low-risk
+Shape 14 program (solution/shape14/defaults.py:22-49) so its config_id can be
+reproduced; its Triton attention is rejected by this build's PlanBuilder.
+
+hip_streamed_config is the gfx950 program for long sequences: HIP streaming
+attention and HIP norms with ordered microbatches (2 sequences per chunk by
+default, the BASELINE long-sequence configuration).
+"""
+
+from __future__ import annotations
+
+from solution.config import (
+    AttentionBackend,
+    AttentionLaunchParams,
+    AttentionOutputBridge,
+    ConfigSpec,
+    FFNBackend,
+    InitialNormBackend,
+    PrecisionPlan,
+    ProgramConfig,
+    ProjectionBackend,
+    QKVMaterialization,
+    ResidualNormBackend,
+    RuntimeBackend,
+    ScheduleConfig,
+    hip_config,
+)
+
+DEFAULT_MICROBATCH_SIZE = 2
+
+
+def conservative_streamed_config() -> ConfigSpec:
+    """The reference's pre-tuning Shape 14 program (Triton attention)."""
+
+    return ConfigSpec(
+        program=ProgramConfig(
+            attention=AttentionBackend.TRITON_STREAMING_DH64,
+            qkv_projection=ProjectionBackend.FP16_SHADOW,
+            attention_output_projection=ProjectionBackend.FP16_SHADOW,
+            ffn_input_projection=ProjectionBackend.FP16_SHADOW,
+            ffn_output_projection=ProjectionBackend.INPUT_DTYPE,
+            precision_plan=PrecisionPlan.FP16_ATTENTION_AND_FFN_INPUT,
+            qkv_materialization=QKVMaterialization.VIEW,
+            attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
+            ffn=FFNBackend.TORCH,
+            residual_norm=ResidualNormBackend.TORCH,
+            initial_norm=InitialNormBackend.TORCH,
+        ),
+        schedule=ScheduleConfig(
+            runtime=RuntimeBackend.STREAMED,
+            attention_launch=AttentionLaunchParams(block_m=32, block_n=64, num_warps=4, num_stages=2),
+            microbatch_size=1,
+        ),
+    )
+
+
+def hip_streamed_config(*, microbatch_size: int = DEFAULT_MICROBATCH_SIZE) -> ConfigSpec:
+    """The gfx950 long-sequence program with ordered microbatches."""
+
+    return hip_config(microbatch_size=microbatch_size)
+
+
+__all__ = ["DEFAULT_MICROBATCH_SIZE", "conservative_streamed_config", "hip_streamed_config"]

@@ -1,0 +1,181 @@
+"""GPU parity of the whole plugin model on the HIP plan.
+
+"The reference PyTorch path on the same seeded inputs" is the oracle's
+official-order forward in the model dtype (bf16 weights and activations,
+fp32 softmax and statistics).  Gate, elementwise (oracle.compare): bf16 or
+fp16 outputs pass when |err| <= 2e-2 or |err| <= 1e-2 * |ref|; fp32 outputs
+when |err| <= 1e-4 or |err| <= 1e-4 * |ref|.  A second, looser comparison
+against the fp32 forward of the same rounded weights is reported in the
+failure message.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.compare import official_compare, parity_gate
+from oracle.forward import TransformerConfig, cast_state, forward, generate_input, xavier_init_weights
+
+pytestmark = pytest.mark.gpu
+
+
+class _StateSource(torch.nn.Module):
+    def __init__(self, tensors):
+        super().__init__()
+        self._tensors = tensors
+
+    def state_dict(self, *args, **kwargs):
+        return dict(self._tensors)
+
+
+def _model(config, state, device, dtype):
+    from solution.transformer import UserOptimizedTransformer, copy_model_weights
+
+    model = UserOptimizedTransformer(config)
+    copy_model_weights(_StateSource(state), model)
+    return model.to(device=device, dtype=dtype).eval()
+
+
+def _check(reference, output, dtype, what, fp32_reference=None):
+    result = parity_gate(reference, output.float().cpu(), dtype)
+    extra = ""
+    if fp32_reference is not None:
+        loose = official_compare(fp32_reference, output.float().cpu(), rtol=0.02, atol=0.02)
+        extra = f"; vs fp32 forward max_abs={loose.max_abs_error:.4g} failed={loose.failed_elements}"
+    print(f"{what}: max_abs={result.max_abs_error:.4g} failed={result.failed_elements}{extra}", flush=True)
+    assert result.passed, f"{what}: {result.failed_elements}/{result.total_elements} failed, max_abs={result.max_abs_error:.4g} at {result.worst_index}{extra}"
+
+
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 256, 512, 8, 2048, 2),   # BASELINE config 2 widths, fewer sequences
+        (1, 300, 1024, 16, 4096, 2),  # long-sequence widths, ragged length
+        (2, 128, 2048, 32, 8192, 1),  # config 4 widths
+    ],
+)
+def test_hip_plan_matches_the_bf16_reference_path(gpu_device, shape):
+    from solution.config import hip_config
+
+    batch, seq, width, heads, ffn, layers = shape
+    print(f"model parity {shape}", flush=True)
+    config = TransformerConfig(batch, seq, width, heads, ffn, layers, True)
+    state = xavier_init_weights(config, seed=1234)
+    x = generate_input(config, seed=1234).to(torch.bfloat16)
+    model = _model(config, state, gpu_device, torch.bfloat16)
+    model.configure_execution(config=hip_config())
+    model.set_execution_observation(True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    torch.cuda.synchronize()
+    reference = forward(cast_state(state, torch.bfloat16), x, config)
+    fp32_reference = forward(cast_state(cast_state(state, torch.bfloat16), torch.float32), x.float(), config)
+    _check(reference, output, torch.bfloat16, f"hip model {shape}", fp32_reference)
+    description = model.describe_execution_path()
+    observed = description["observed_execution_signature"]
+    assert observed == description["expected_execution_signature"]
+    assert observed["attention_backend"] == "hip_streaming_dh64"
+    assert observed["residual_norm_backend"] == "hip_fused"
+    assert observed["initial_norm_backend"] == "hip"
+
+
+def test_streamed_output_equals_its_chunks_bitwise(gpu_device):
+    """The streamed driver runs ordered chunks and writes each chunk's final
+    norm into the logical output: identical to running the chunks alone."""
+
+    from solution.config import hip_config
+
+    config = TransformerConfig(4, 200, 512, 8, 2048, 2, True)
+    state = xavier_init_weights(config, seed=7)
+    x = generate_input(config, seed=7).to(torch.bfloat16).to(gpu_device)
+    streamed = _model(config, state, gpu_device, torch.bfloat16)
+    streamed.configure_execution(config=hip_config(microbatch_size=2))
+    eager = _model(TransformerConfig(2, 200, 512, 8, 2048, 2, True), state, gpu_device, torch.bfloat16)
+    eager.configure_execution(config=hip_config())
+    with torch.inference_mode():
+        whole = streamed(x)
+        parts = torch.cat([eager(x[0:2]), eager(x[2:4])])
+    assert torch.equal(whole, parts)
+    assert streamed.describe_execution_path()["runtime_backend"] == "streamed"
+
+
+def test_long_sequence_forward_prefix_matches_the_oracle(gpu_device):
+    """A 100 000-token forward at the long-sequence configuration's widths
+    (D1024 H16 F4096 L2, bf16).  Causality makes its first rows a function of
+    the prefix only, so they are checked against the oracle on that prefix."""
+
+    from solution.config import hip_config
+
+    seq, prefix = 100_000, 1024
+    config = TransformerConfig(1, seq, 1024, 16, 4096, 2, True)
+    state = xavier_init_weights(config, seed=2024)
+    x = generate_input(config, seed=2024).to(torch.bfloat16)
+    model = _model(config, state, gpu_device, torch.bfloat16)
+    model.configure_execution(config=hip_config(microbatch_size=1))
+    print("long-sequence forward S=100000", flush=True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    torch.cuda.synchronize()
+    assert torch.isfinite(output).all()
+    prefix_config = TransformerConfig(1, prefix, 1024, 16, 4096, 2, True)
+    reference = forward(cast_state(state, torch.bfloat16), x[:, :prefix], prefix_config)
+    _check(reference, output[:, :prefix], torch.bfloat16, "S=100000 prefix rows")
+
+
+def test_reference_shape14_program_with_hip_kernels_on_an_fp32_model(gpu_device):
+    """The reference's deployed mixed-precision program (fp32 I/O, FP16 shadow
+    projections) with the attention and norms swapped to the HIP kernels."""
+
+    from solution.config import (
+        AttentionLaunchParams,
+        ConfigSpec,
+        NormLaunchParams,
+        ProgramConfig,
+        RuntimeBackend,
+        ScheduleConfig,
+    )
+
+    config = TransformerConfig(2, 256, 512, 8, 2048, 2, True)
+    state = xavier_init_weights(config, seed=3)
+    x = generate_input(config, seed=3)
+    program = ProgramConfig(
+        attention="hip_streaming_dh64",
+        qkv_projection="fp16_shadow",
+        attention_output_projection="fp16_shadow",
+        ffn_input_projection="fp16_shadow",
+        ffn_output_projection="fp16_shadow",
+        precision_plan="fp16_core",
+        qkv_materialization="view",
+        attention_output_bridge="attention_direct_bsd",
+        ffn="torch",
+        residual_norm="hip_mixed",
+        initial_norm="hip",
+    )
+    schedule = ScheduleConfig(
+        runtime=RuntimeBackend.EAGER,
+        attention_launch=AttentionLaunchParams(128, 64, 4, 2),
+        residual_norm_launch=NormLaunchParams(4, 4),
+        initial_norm_launch=NormLaunchParams(4, 4),
+    )
+    model = _model(config, state, gpu_device, torch.float32)
+    model.configure_execution(config=ConfigSpec(program=program, schedule=schedule))
+    model.set_execution_observation(True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    assert output.dtype == torch.float32
+    reference = forward(state, x, config)
+    _check(reference, output, torch.float16, "mixed fp16 program")
+    observed = model.describe_execution_path()["observed_execution_signature"]
+    assert observed["residual_norm_backend"] == "hip_mixed" and observed["complete"]
+
+
+def test_default_resolution_on_gfx950_selects_the_hip_program(gpu_device):
+    from solution.config import hip_config
+
+    config = TransformerConfig(2, 64, 512, 8, 1024, 1, True)
+    model = _model(config, xavier_init_weights(config, seed=1), gpu_device, torch.bfloat16)
+    x = generate_input(config, seed=1).to(torch.bfloat16).to(gpu_device)
+    with torch.inference_mode():
+        model(x)
+    assert model.describe_execution_path()["planned_config_id"] == hip_config().config_id

@@ -1,0 +1,85 @@
+"""The C ABI: header declarations, exported symbols and host-side checks.
+
+No kernel is launched here: only entry points that never touch the device
+(version, launch-table queries, workspace sizing, argument validation that
+fails before any launch) are called.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from solution.kernels.hip import _library
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "shape_aware_hip.h"
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(sah_[a-z_0-9]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    declared = _declared_functions()
+    assert declared == set(_library.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    if not _library.LIBRARY_PATH.exists():
+        pytest.fail(f"{_library.LIBRARY_PATH} is not built; run __graft_entry__.build()")
+    raw = ctypes.CDLL(str(_library.LIBRARY_PATH))
+    for name in _declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_host_only_entry_points():
+    library = _library.load_library()
+    assert library.sah_abi_version() == _library.ABI_VERSION
+    assert library.sah_causal_attention_launch_supported(128, 64, 4, 2) == 1
+    assert library.sah_causal_attention_launch_supported(256, 64, 4, 1) == 1
+    assert library.sah_causal_attention_launch_supported(64, 64, 4, 2) == 0
+    # V given head_dim-contiguous needs a V^T workspace padded to 64 keys.
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 3072, 1, 2) == 2 * 16 * 64 * 100032 * 2
+    # seq-contiguous V (a V^T buffer) needs none.
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 1, 100032, 2) == 0
+
+
+def test_invalid_arguments_fail_before_launch():
+    library = _library.load_library()
+    status = library.sah_causal_attention_bsd(
+        None, None, None, None, 1, 1, 1, 64, *([0] * 12), 0.125, 2, 128, 64, 4, 2, None, 0, None
+    )
+    assert status == _library.SAH_ERR_INVALID_ARGUMENT
+    assert b"non-null" in library.sah_last_error()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    status = library.sah_causal_attention_bsd(
+        fake, fake, fake, fake, 1, 1, 16, 32, *([0] * 12), 0.125, 2, 128, 64, 4, 2, None, 0, None
+    )
+    assert status == _library.SAH_ERR_UNSUPPORTED and b"head_dim" in library.sah_last_error()
+    status = library.sah_residual_norm(
+        fake, fake, None, None, fake, fake, 4, 1000, 1e-5, 2, 2, 2, 0, 0, 4, 4, None
+    )
+    assert status == _library.SAH_ERR_UNSUPPORTED
+    status = library.sah_norm(fake, None, None, fake, 4, 1024, 1e-5, 2, 2, 0, 7, 4, 4, None)
+    assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"norm kind" in library.sah_last_error()
+    status = library.sah_norm(fake, None, None, fake, 4, 1024, 1e-5, 2, 2, 0, 0, 3, 2, None)
+    assert status == _library.SAH_ERR_UNSUPPORTED
+    with pytest.raises(_library.HipLibraryError, match="status 2"):
+        _library.check_status(_library.SAH_ERR_UNSUPPORTED, "probe")
+
+
+def test_custom_op_has_a_fake_implementation():
+    """The attention op traces on meta tensors (no kernel runs)."""
+
+    import torch
+
+    from solution.shape14 import hip_streaming_dh64  # noqa: F401 - registers the op
+
+    q = torch.empty(2, 16, 1000, 64, device="meta", dtype=torch.bfloat16)
+    out = torch.ops.shape_aware_hip.streaming_dh64_causal_attention_bsd(q, q, q, 0.125, 128, 64, 4, 2)
+    assert out.shape == (2, 1000, 1024) and out.device.type == "meta"

@@ -1,0 +1,214 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+Each oracle function is checked against something that does not share its
+code: float64 library routines, scalar-loop brute force, the reference's own
+known answers, or invariants a plausible mistake would break.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import norm as oracle_norm
+from oracle.compare import OFFICIAL_ATOL, OFFICIAL_RTOL, official_compare, parity_gate
+from oracle.forward import (
+    TransformerConfig,
+    causal_attention_rows,
+    default_init_weights,
+    dense_causal_attention,
+    forward,
+    generate_input,
+    query_block_causal_attention,
+    xavier_init_weights,
+)
+from oracle.workload import (
+    C3_ATTENTION,
+    C3_NORM,
+    C5,
+    causal_attention_flops,
+    estimated_model_flops,
+    residual_norm_bytes,
+)
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+C1 = TransformerConfig(2, 128, 256, 4, 1024, 2, True)
+
+
+def test_c1_forward_matches_float64_library_golden():
+    """Official op order in fp32 vs float64 SDPA/layer_norm/gelu (config 1)."""
+
+    golden = np.load(GOLDEN / "c1_forward.npz")
+    state = default_init_weights(C1, seed=1234)
+    sums = np.array([float(state[name].double().sum()) for name in golden["weight_names"]])
+    np.testing.assert_allclose(sums, golden["weight_sums"], rtol=0, atol=1e-9)
+    x = generate_input(C1, seed=1234)
+    assert np.array_equal(x.numpy(), golden["x"])
+    out = forward(state, x, C1)
+    result = parity_gate(torch.from_numpy(golden["out"]), out, torch.float32)
+    assert result.passed, result
+    assert result.max_abs_error < 2e-5
+
+
+def test_dense_attention_matches_scalar_loop_golden():
+    golden = np.load(GOLDEN / "tiny_attention.npz")
+    q, k, v = (torch.from_numpy(golden[name]) for name in ("q", "k", "v"))
+    out = dense_causal_attention(q, k, v, 1 / math.sqrt(4))
+    # the official order runs the softmax in fp32 even for float64 scores
+    np.testing.assert_allclose(out.numpy(), golden["out"], rtol=2e-6, atol=2e-6)
+
+
+def test_query_block_order_equals_dense_order():
+    """Restates the reference's check that the query-block path keeps the
+    official operation order (tests/solution/test_causal_operators.py:62-84)."""
+
+    generator = torch.Generator().manual_seed(19)
+    q, k, v = (torch.randn(2, 2, 300, 16, generator=generator) for _ in range(3))
+    dense = dense_causal_attention(q, k, v, 0.25)
+    for block in (1, 7, 128, 300, 512):
+        torch.testing.assert_close(query_block_causal_attention(q, k, v, 0.25, query_block=block), dense)
+
+
+def test_attention_matches_torch_sdpa_float64():
+    generator = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(2, 3, 50, 64, generator=generator, dtype=torch.float64) for _ in range(3))
+    expected = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125)
+    # fp32 softmax inside the official order bounds the agreement at fp32 level
+    torch.testing.assert_close(dense_causal_attention(q, k, v, 0.125), expected, rtol=1e-6, atol=1e-6)
+
+
+def test_attention_rows_match_dense_float64():
+    generator = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(1, 1, 200, 64, generator=generator, dtype=torch.float64) for _ in range(3))
+    dense = dense_causal_attention(q, k, v, 0.125)[0, 0].numpy()
+    rows = np.array([0, 1, 99, 199])
+    got = causal_attention_rows(q[0, 0].numpy(), k[0, 0].numpy(), v[0, 0].numpy(), rows, 0.125)
+    np.testing.assert_allclose(got, dense[rows], rtol=1e-6, atol=1e-6)
+    exact = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125)[0, 0].numpy()
+    np.testing.assert_allclose(got, exact[rows], rtol=1e-12, atol=1e-12)
+
+
+def test_attention_mask_side_and_first_row():
+    """Row 0 sees only key 0; a mistake on the mask side changes both checks."""
+
+    generator = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(1, 1, 10, 8, generator=generator, dtype=torch.float64) for _ in range(3))
+    out = dense_causal_attention(q, k, v, 1.0)
+    torch.testing.assert_close(out[0, 0, 0], v[0, 0, 0])
+    k2 = k.clone()
+    k2[0, 0, 9] += 100.0  # change the last key: every row before it is unaffected
+    v2 = v.clone()
+    v2[0, 0, 9] -= 50.0
+    out2 = dense_causal_attention(q, k2, v2, 1.0)
+    torch.testing.assert_close(out2[0, 0, :9], out[0, 0, :9])
+    assert not torch.allclose(out2[0, 0, 9], out[0, 0, 9])
+
+
+def test_layer_norm_matches_scalar_loop_golden_and_library():
+    golden = np.load(GOLDEN / "tiny_layer_norm.npz")
+    value, update, weight, bias = (torch.from_numpy(golden[n]) for n in ("value", "update", "weight", "bias"))
+    residual, normalized = oracle_norm.residual_layer_norm(value, update, weight, bias)
+    np.testing.assert_allclose(normalized.numpy(), golden["out"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(residual.numpy(), golden["value"] + golden["update"], rtol=0, atol=0)
+    library = F.layer_norm(value + update, (8,), weight, bias, 1e-5)
+    torch.testing.assert_close(normalized, library)
+    row = oracle_norm.layer_norm_loop(golden["value"][1] + golden["update"][1], golden["weight"], golden["bias"], 1e-5)
+    np.testing.assert_allclose(row, golden["out"][1], rtol=1e-12, atol=1e-12)
+
+
+def test_residual_is_rounded_to_the_stream_dtype_before_normalizing():
+    value = torch.tensor([[1.0, 2.0, 3.0, 4.0]], dtype=torch.bfloat16)
+    update = torch.tensor([[1e-3, -1e-3, 1e-3, 0.0]], dtype=torch.bfloat16)
+    residual, normalized = oracle_norm.residual_layer_norm(value, update, None, None)
+    assert residual.dtype == torch.bfloat16
+    assert torch.equal(residual, (value.double() + update.double()).to(torch.bfloat16))
+    expected = oracle_norm.layer_norm(residual, None, None)
+    assert torch.equal(normalized, expected)
+
+
+def test_rms_norm_matches_library():
+    generator = torch.Generator().manual_seed(6)
+    x = torch.randn(5, 32, generator=generator, dtype=torch.float64)
+    w = torch.randn(32, generator=generator, dtype=torch.float64)
+    torch.testing.assert_close(oracle_norm.rms_norm(x, w, 1e-6), F.rms_norm(x, (32,), w, 1e-6))
+
+
+def test_constant_row_normalizes_to_bias():
+    x = torch.full((2, 16), 3.0, dtype=torch.float64)
+    b = torch.arange(16, dtype=torch.float64)
+    assert torch.equal(oracle_norm.layer_norm(x, torch.ones(16, dtype=torch.float64), b), b.expand(2, 16))
+
+
+def test_official_comparator_is_an_or_rule():
+    reference = torch.tensor([1.0, 100.0, 0.0, 1.0])
+    candidate = torch.tensor([1.0015, 101.5, 0.0019, float("nan")])
+    result = official_compare(reference, candidate, rtol=OFFICIAL_RTOL, atol=OFFICIAL_ATOL)
+    # 1.0015: abs ok; 101.5: rel 1.5% ok; 0.0019: abs ok; nan fails.
+    assert result.failed_elements == 1
+    strict = official_compare(reference[:3], candidate[:3], rtol=0.01, atol=0.001)
+    assert strict.failed_elements == 2  # 101.5 (1.5%) and 0.0019 fail; 1.0015 passes on rel
+    # |err| = 0.021 at ref 1: fails the OR rule although atol + rtol*|ref| = 0.022 would pass.
+    summed = official_compare(torch.tensor([1.0]), torch.tensor([1.021]), rtol=0.02, atol=0.002)
+    assert not summed.passed
+    assert OFFICIAL_RTOL == 0.02 and OFFICIAL_ATOL == 0.002
+
+
+def test_flop_models_reproduce_reference_known_answers():
+    # tests/benchmarking/test_shape14_measure.py:45-48 of the reference
+    assert estimated_model_flops(batch=8, seq=16, width=32, ffn=32, layers=2) == 3_407_872
+    # final_performance.json:421 of the reference (official Shape 14, F=1024)
+    assert estimated_model_flops(batch=32, seq=100000, width=1024, ffn=1024, layers=2) == 1_391_250_636_800_000
+    b, h, s, d = C3_ATTENTION
+    assert causal_attention_flops(b, h, s, d) == 68_753_031_168
+    assert causal_attention_flops(2, 16, 100000, 64) * 16 * C5.num_layers == 1_310_733_107_200_000
+    # brute force on a tiny causal triangle: QK^T and PV each 2*Dh per pair
+    pairs = sum(i + 1 for i in range(5))
+    assert causal_attention_flops(1, 1, 5, 3) == 4 * 3 * pairs
+    rows, width = C3_NORM
+    assert residual_norm_bytes(rows, width, params=0) == 134_217_728
+
+
+def test_seeded_inputs_follow_the_official_generator():
+    config = TransformerConfig(2, 3, 4, 2, 8, 1, True)
+    generator = torch.Generator().manual_seed(99)
+    expected = torch.randn(2, 3, 4, generator=generator) * 0.5
+    assert torch.equal(generate_input(config, 99, input_scale=0.5), expected)
+
+
+def test_default_init_follows_linear_init_bounds():
+    state = default_init_weights(TransformerConfig(1, 4, 64, 4, 128, 1, True), seed=0)
+    bound = 1 / math.sqrt(64)
+    assert state["layers.0.attention.q_proj.weight"].abs().max() <= bound
+    assert state["layers.0.ffn_out.weight"].abs().max() <= 1 / math.sqrt(128)
+    assert torch.equal(state["layers.0.norm1.weight"], torch.ones(64))
+    assert torch.equal(state["final_norm.bias"], torch.zeros(64))
+
+
+def test_xavier_init_bounds_and_zero_biases():
+    config = TransformerConfig(1, 4, 64, 4, 256, 2, True)
+    state = xavier_init_weights(config, seed=1)
+    bound = math.sqrt(6 / (64 + 256))
+    weight = state["layers.1.ffn_in.weight"]
+    assert weight.shape == (256, 64) and weight.abs().max() <= bound
+    assert weight.abs().max() > 0.9 * bound
+    assert torch.equal(state["layers.0.attention.out_proj.bias"], torch.zeros(64))
+    assert torch.equal(xavier_init_weights(config, seed=1)["layers.0.attention.q_proj.weight"],
+                       state["layers.0.attention.q_proj.weight"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_forward_prefix_is_causal(dtype):
+    """Rows before t do not depend on tokens at or after t (the property the
+    long-sequence GPU test uses to check a 100k-token forward on a prefix)."""
+
+    config = TransformerConfig(1, 40, 64, 4, 128, 2, True)
+    state = default_init_weights(config, seed=3)
+    x = generate_input(config, 3).to(dtype)
+    full = forward(state, x, config)
+    prefix = forward(state, x[:, :25], TransformerConfig(1, 25, 64, 4, 128, 2, True))
+    assert torch.equal(full[:, :25], prefix)

@@ -1,0 +1,310 @@
+"""Plan API: config format and ids, legality, streamed schedule (CPU only)."""
+
+from __future__ import annotations
+
+import dataclasses
+import json
+from pathlib import Path
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from solution.config import (
+    AttentionBackend,
+    AttentionLaunchParams,
+    ConfigSpec,
+    InitialNormBackend,
+    NormLaunchParams,
+    ProgramConfig,
+    ResidualNormBackend,
+    RuntimeBackend,
+    ScheduleConfig,
+    TritonAttentionParams,
+    hip_config,
+    portable_config,
+    portable_streamed_config,
+)
+from solution.plan import ExecutionContext
+from solution.plan_builder import ConfigRejectedError, HardwareCapabilities, PlanBuilder
+from solution.shape14.defaults import conservative_streamed_config, hip_streamed_config
+from solution.shape14.executor import execute_streamed
+from solution.transformer import _is_official_shape14, _uses_streamed_scope
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _gfx950(**overrides) -> HardwareCapabilities:
+    values = dict(
+        device_type="cuda",
+        compute_capability=(9, 5),
+        shared_memory_per_block=65536,
+        mem_efficient_sdp=False,
+        cudnn_sdp=False,
+        cudnn_available=False,
+        torch_compile=False,
+        triton_shape13_attention=False,
+        triton_dh8_attention=False,
+        triton_residual_norm=False,
+        triton_mixed_residual_norm=False,
+        triton_initial_norm=False,
+        triton_exact_gelu=False,
+        triton_streaming_dh64_attention=False,
+        gcn_arch="gfx950",
+        hip_streaming_dh64_attention=True,
+        hip_residual_norm=True,
+        hip_initial_norm=True,
+    )
+    values.update(overrides)
+    return HardwareCapabilities(**values)
+
+
+def _context(batch=32, seq=100000, d=1024, heads=16, ffn=4096, layers=2, *, dtype=torch.bfloat16,
+             device="cuda", mask=False, grad=False) -> ExecutionContext:
+    return ExecutionContext(
+        batch_size=batch,
+        seq_len=seq,
+        d_model=d,
+        num_heads=heads,
+        causal=True,
+        device=torch.device(device),
+        dtype=dtype,
+        training=False,
+        grad_enabled=grad,
+        input_contiguous=True,
+        has_valid_token_mask=mask,
+        mask_compatible=True,
+        ffn_dim=ffn,
+        num_layers=layers,
+    )
+
+
+# ---------------------------------------------------------------- config ids
+
+
+def test_reference_config_ids_are_reproduced():
+    """Golden ids: tests/benchmarking/test_shape14_defaults.py:12-13 and the
+    deployed Shape 14 program (final_performance.json:407) of the reference."""
+
+    assert conservative_streamed_config().config_id == (
+        "cfg-3d94f979e8424ea78bfd0656a0d32182cb9f0e706f85b805e6d01571496b75ec"
+    )
+    assert conservative_streamed_config().schedule.attention_launch.to_dict() == {
+        "block_m": 32, "block_n": 64, "num_warps": 4, "num_stages": 2,
+    }
+
+
+def test_every_reference_deployed_config_round_trips_with_its_published_id():
+    records = json.loads((GOLDEN / "reference_configs.json").read_text())["records"]
+    assert len(records) == 14
+    for record in records:
+        config = ConfigSpec.from_dict(record["config"])
+        assert config.to_dict() == record["config"]
+        assert config.config_id == record["published_config_id"], record["case_id"]
+    shape14 = ConfigSpec.from_dict(records[-1]["config"])
+    assert shape14.config_id == "cfg-cc77d6b483e1f07e137d89773db64dd8a3367f901dbae918aa7cebffd405ab60"
+
+
+def test_canonical_json_is_sorted_compact_ascii():
+    text = portable_config().canonical_json()
+    assert " " not in text and text.isascii()
+    assert text == json.dumps(json.loads(text), sort_keys=True, separators=(",", ":"))
+    assert portable_config().config_id == "cfg-" + portable_config().sha256
+
+
+def test_hip_config_round_trips_and_uses_existing_fields():
+    config = hip_config(microbatch_size=2)
+    payload = config.to_dict()
+    assert set(payload["schedule"]) == set(portable_config().to_dict()["schedule"])
+    assert ConfigSpec.from_dict(json.loads(json.dumps(payload))) == config
+    assert payload["program"]["attention"] == "hip_streaming_dh64"
+    assert payload["program"]["residual_norm"] == "hip_fused"
+    assert payload["program"]["initial_norm"] == "hip"
+    assert config.config_id == hip_streamed_config().config_id
+    assert TritonAttentionParams is AttentionLaunchParams
+
+
+def test_presence_rules_cover_hip_backends():
+    program = hip_config().program
+    with pytest.raises(ValueError, match="attention_launch"):
+        ConfigSpec(program=program, schedule=ScheduleConfig(runtime=RuntimeBackend.EAGER))
+    with pytest.raises(ValueError, match="residual_norm_launch"):
+        ConfigSpec(
+            program=program,
+            schedule=ScheduleConfig(
+                runtime=RuntimeBackend.EAGER,
+                attention_launch=AttentionLaunchParams(128, 64, 4, 2),
+                initial_norm_launch=NormLaunchParams(4, 4),
+            ),
+        )
+
+
+@pytest.mark.parametrize(
+    "field,payload",
+    [
+        ("attention_launch", {"block_m": 96, "block_n": 64, "num_warps": 4, "num_stages": 2}),
+        ("attention_launch", {"block_m": 128, "block_n": 64, "num_warps": 3, "num_stages": 2}),
+        ("attention_launch", {"block_m": 128, "block_n": 64, "num_warps": 4}),
+        ("residual_norm_launch", {"block_rows": 4, "num_warps": 4, "extra": 1}),
+    ],
+)
+def test_launch_objects_are_exact_and_validated(field, payload):
+    document = hip_config().to_dict()
+    document["schedule"][field] = payload
+    with pytest.raises((ValueError, TypeError)):
+        ConfigSpec.from_dict(document)
+
+
+# ---------------------------------------------------------------- legality
+
+
+def test_hip_plan_is_accepted_for_the_long_sequence_configuration():
+    plan = PlanBuilder().build(hip_streamed_config(), _context(), _gfx950())
+    assert plan.use_streamed_execution
+    assert plan.inner_context.batch_size == 2 and plan.outer_context.batch_size == 32
+    assert plan.attention_compute_dtype == "bfloat16"
+    trace = plan.expected_trace.to_dict()
+    assert trace["attention_calls"] == 2 and trace["residual_norm_calls"] == 4
+    assert trace["initial_norm_calls"] == 1 and trace["complete"] is True
+    description = plan.describe()
+    assert description["causal_mask"] == "online_causal"
+    assert description["inner_batch_size"] == 2
+
+
+def test_hip_plan_rejections_are_structured():
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    cpu = builder.evaluate(hip_config(), _context(device="cpu"), _gfx950(device_type="cpu", gcn_arch=None))
+    assert ("program.attention", "requires_cuda") in codes(cpu)
+    mi300 = builder.evaluate(hip_config(), _context(), _gfx950(gcn_arch="gfx942"))
+    assert ("program.attention", "requires_gfx950") in codes(mi300)
+    wide_heads = builder.evaluate(hip_config(), _context(heads=8), _gfx950())
+    assert ("program.attention", "unsupported_shape") in codes(wide_heads)
+    fp32 = builder.evaluate(hip_config(), _context(dtype=torch.float32), _gfx950())
+    assert ("program.qkv_projection", "requires_16bit_qkv") in codes(fp32)
+    missing = builder.evaluate(hip_config(), _context(), _gfx950(hip_streaming_dh64_attention=False,
+                                                                  hip_residual_norm=False))
+    assert ("program.attention", "backend_unavailable") in codes(missing)
+    assert ("program.residual_norm", "backend_unavailable") in codes(missing)
+    grad = builder.evaluate(hip_config(), _context(grad=True), _gfx950())
+    assert ("program.attention", "requires_inference") in codes(grad)
+    odd_width = builder.evaluate(hip_config(), _context(d=1000, heads=10), _gfx950())
+    assert ("program.residual_norm", "unsupported_shape") in codes(odd_width)
+    with pytest.raises(ConfigRejectedError, match="program.attention"):
+        builder.build(hip_config(), _context(heads=8), _gfx950())
+
+
+def test_streamed_microbatch_rules():
+    builder = PlanBuilder()
+    for batch, microbatch, code in ((6, 4, "microbatch_not_divisor"), (2, 4, "microbatch_exceeds_batch")):
+        result = builder.evaluate(hip_config(microbatch_size=microbatch), _context(batch=batch), _gfx950())
+        assert ("schedule.microbatch_size", code) in {(v.field, v.code) for v in result.violations}
+    masked = builder.evaluate(hip_config(microbatch_size=2), _context(mask=True), _gfx950())
+    assert ("schedule.runtime", "mask_not_supported") in {(v.field, v.code) for v in masked.violations}
+
+
+def test_reference_only_backends_are_unavailable_not_silently_replaced():
+    records = json.loads((GOLDEN / "reference_configs.json").read_text())["records"]
+    builder = PlanBuilder()
+    shape14 = ConfigSpec.from_dict(records[-1]["config"])
+    result = builder.evaluate(shape14, _context(dtype=torch.float32, ffn=1024), _gfx950())
+    assert not result.accepted
+    assert ("program.attention", "backend_unavailable") in {(v.field, v.code) for v in result.violations}
+    # the reference's deployed Shape 14 program with only the attention swapped is legal
+    program = ProgramConfig.from_dict({**records[-1]["config"]["program"], "attention": "hip_streaming_dh64"})
+    schedule = dataclasses.replace(shape14.schedule, attention_launch=AttentionLaunchParams(128, 64, 4, 2))
+    swapped = ConfigSpec(program=program, schedule=schedule)
+    plan = builder.build(swapped, _context(dtype=torch.float32, ffn=1024), _gfx950())
+    assert plan.attention_compute_dtype == "float16"  # FP16 shadow QKV feeds the HIP kernel
+
+
+def test_portable_configs_are_legal_on_cpu():
+    cpu = _gfx950(device_type="cpu", gcn_arch=None, hip_streaming_dh64_attention=False)
+    plan = PlanBuilder().build(portable_config(), _context(batch=2, seq=16, d=64, heads=4, device="cpu",
+                                                           dtype=torch.float32), cpu)
+    assert plan.attention_backend is AttentionBackend.REFERENCE_STREAMING
+    assert plan.describe()["causal_mask"] == "query_block"
+
+
+def test_mixed_stream_plan_requires_fp16_updates():
+    program = ProgramConfig(
+        attention=AttentionBackend.HIP_STREAMING_DH64,
+        qkv_projection="fp16_shadow",
+        attention_output_projection="fp16_shadow",
+        ffn_input_projection="fp16_shadow",
+        ffn_output_projection="fp16_shadow",
+        precision_plan="fp16_core",
+        qkv_materialization="view",
+        attention_output_bridge="attention_direct_bsd",
+        ffn="torch",
+        residual_norm=ResidualNormBackend.HIP_MIXED,
+        initial_norm=InitialNormBackend.HIP,
+    )
+    schedule = ScheduleConfig(
+        runtime=RuntimeBackend.EAGER,
+        attention_launch=AttentionLaunchParams(128, 64, 4, 2),
+        residual_norm_launch=NormLaunchParams(4, 4),
+        initial_norm_launch=NormLaunchParams(4, 4),
+    )
+    plan = PlanBuilder().build(ConfigSpec(program=program, schedule=schedule),
+                               _context(dtype=torch.float32), _gfx950())
+    assert plan.use_mixed_residual_stream
+    bf16 = PlanBuilder().evaluate(ConfigSpec(program=program, schedule=schedule), _context(), _gfx950())
+    assert ("program.residual_norm", "requires_float32_input") in {(v.field, v.code) for v in bf16.violations}
+
+
+# ------------------------------------------------------------ streamed driver
+
+
+def test_official_shape14_and_long_sequences_use_the_streamed_scope():
+    """Restates tests/solution/test_shape14_isolation.py:18-27 of the reference
+    and adds the F=4096 long-sequence configuration."""
+
+    config = SimpleNamespace(num_heads=16, num_layers=2, ffn_dim=1024, causal=True)
+    assert _is_official_shape14(config, (32, 100000, 1024))
+    assert not _is_official_shape14(config, (1, 100000, 1024))
+    wide = SimpleNamespace(num_heads=16, num_layers=2, ffn_dim=4096, causal=True)
+    assert _uses_streamed_scope(wide, (32, 100000, 1024))
+    assert not _uses_streamed_scope(wide, (64, 256, 512))
+
+
+def test_streamed_executor_preserves_order_and_mask_slices():
+    """Restates tests/solution/test_shape14_isolation.py:56-89."""
+
+    value = torch.arange(24, dtype=torch.float32).reshape(4, 3, 2)
+    mask = torch.tensor([[True, True, True], [True, False, False], [True, True, False], [False, False, False]])
+    seen: list[torch.Tensor] = []
+
+    def forward_chunk(chunk, chunk_mask):
+        seen.append(chunk_mask.clone())
+        return chunk + 1
+
+    output = execute_streamed(value, mask, microbatch_size=2, forward_chunk=forward_chunk)
+    torch.testing.assert_close(output, value + 1)
+    torch.testing.assert_close(torch.cat(seen), mask)
+
+
+@pytest.mark.parametrize("microbatch_size", [0, True, 3])
+def test_streamed_executor_rejects_invalid_microbatches(microbatch_size):
+    with pytest.raises(ValueError):
+        execute_streamed(torch.zeros(4, 2, 1), None, microbatch_size=microbatch_size,
+                         forward_chunk=lambda chunk, mask: chunk)
+
+
+def test_streamed_executor_writes_chunks_into_the_preallocated_output():
+    value = torch.arange(32, dtype=torch.float32).reshape(8, 2, 2)
+    destinations: list[int] = []
+
+    def forward_chunk(chunk, mask, destination):
+        destinations.append(destination.data_ptr())
+        torch.mul(chunk, 2, out=destination)
+        return destination
+
+    output = execute_streamed(value, None, microbatch_size=2, forward_chunk=forward_chunk,
+                              write_into_output=True)
+    assert torch.equal(output, value * 2)
+    assert destinations == [output[i:i + 2].data_ptr() for i in range(0, 8, 2)]
+    copied = execute_streamed(value, None, microbatch_size=4,
+                              forward_chunk=lambda chunk, mask, destination: chunk - 1,
+                              write_into_output=True)
+    assert torch.equal(copied, value - 1)
