@@ -323,6 +323,264 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
+// Cross-half reductions: lanes l and l^32 hold the two key halves of one
+// query row.  v_permlane32_swap exchanges the halves of two registers; the max
+// (or sum) of the two results is the cross-half value in every lane, whichever
+// half each register received.
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Software-pipelined variant (num_stages == 3).  Iteration j computes
+// S^T(j) and its softmax while the PV product of tile j-1 runs on the MFMA
+// pipe: P(j-1) stays in registers for one iteration, V^T tiles are kept in
+// three LDS stages (tile j-1 is still read while tile j+1 is being written)
+// and K tiles in two.  Every PV term is accumulated at the scale of the
+// running maximum it was computed with; the rescale of O by exp(m_old - m_new)
+// is applied at the end of the iteration, after PV(j-1), and skipped when no
+// row of the wave raised its maximum.  Full, unmasked tiles run a body with no
+// branches between the two MFMA groups and the softmax, so the compiler can
+// interleave MFMA and VALU; the first/last tiles of a wave and the diagonal
+// tiles take a general body.  Full tiles load without per-element guards.
+template <typename T>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_pipelined_kernel(AttnParams p) {
+  typedef typename Vec8<T>::type V8;
+  typedef typename Vec8<T>::half_type V4;
+  typedef typename Vec8<T>::pair_type V2;
+  constexpr int BM = kWaves * 32;
+
+  __shared__ __attribute__((aligned(16))) T k_lds[2][kBlockN][kKRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[3][kHeadDim][kVRow];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+
+  const int bid = blockIdx.x;
+  const int nb = p.num_blocks;
+  const int xcd = bid & 7;
+  const int local = bid >> 3;
+  const int per = nb >> 3;
+  const int rem = nb & 7;
+  const int logical =
+      xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int bh = logical / p.num_q_tiles;
+  const int q_tile = p.num_q_tiles - 1 - (logical - bh * p.num_q_tiles);
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  const int S = p.seq_len;
+
+  const T* qbase = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh;
+  const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
+  const T* vbase = static_cast<const T*>(p.vt) + b * p.v_sb + h * p.v_sh;
+  T* obase = static_cast<T*>(p.o) + b * p.o_sb + (int64_t)h * kHeadDim;
+
+  const int q0 = q_tile * BM;
+  const int wq0 = q0 + wave * 32;
+  const int wq_last = (wq0 < S) ? min(wq0 + 32, S) - 1 : -1;
+  const int key_end = min(q0 + BM, S);
+  const int n_tiles = (key_end + kBlockN - 1) / kBlockN;
+  // Tiles this wave computes: [0, w_tiles); tiles from j_mask on need the mask.
+  const int w_tiles = wq_last < 0 ? 0 : wq_last / kBlockN + 1;
+  const int j_mask = wq0 / kBlockN;  // first tile with a key above some row of the wave
+  const int qi = wq0 + l32;
+
+  V8 qop[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
+    qop[s] = __builtin_bit_cast(V8, raw);
+  }
+
+  u32x4 k_pref[2], v_pref[2];
+  auto load_tile = [&](int tile) {
+    const int k0 = tile * kBlockN;
+    if (k0 + kBlockN <= S) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int chunk = tid + kThreads * i;
+        const int row = chunk >> 3;
+        const int c8 = (chunk & 7) * 8;
+        k_pref[i] = load16(kbase + (int64_t)(k0 + row) * p.k_ss + c8);
+        v_pref[i] = load16(vbase + (int64_t)row * p.v_sd + k0 + c8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int chunk = tid + kThreads * i;
+        const int row = chunk >> 3;
+        const int c8 = (chunk & 7) * 8;
+        const int key = k0 + row;
+        u32x4 raw = {0u, 0u, 0u, 0u};
+        if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
+        k_pref[i] = raw;
+        v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
+                                     (int64_t)k0 + c8, S);
+      }
+    }
+  };
+  auto store_tile = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int row = chunk >> 3;
+      const int c8 = (chunk & 7) * 8;
+      *reinterpret_cast<u32x4*>(&k_lds[tile & 1][row][c8]) = k_pref[i];
+      *reinterpret_cast<u32x4*>(&v_lds[tile % 3][row][c8]) = v_pref[i];
+    }
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[d][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float c = p.c;
+  const int a_row = k_row_for(l32);
+  V8 pb_prev[4];
+
+  // S^T(j) = K(j) Q^T: all eight A operands are read from LDS before the MFMAs.
+  auto scores = [&](int j, f32x16* sacc) {
+    V8 ka[4][2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        ka[s][t] = *reinterpret_cast<const V8*>(&k_lds[j & 1][32 * t + a_row][16 * s + 8 * half]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) sacc[t] = mfma32(ka[0][t], qop[0], f32x16{});
+#pragma unroll
+    for (int s = 1; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) sacc[t] = mfma32(ka[s][t], qop[s], sacc[t]);
+  };
+  // O^T += V^T(j) P^T(j).
+  auto pv = [&](int j, const V8* pb) {
+    const int vs = j % 3;
+    V8 va[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+        va[u][d] = *reinterpret_cast<const V8*>(&v_lds[vs][32 * d + l32][16 * u + 8 * half]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) acc[d] = mfma32(va[u][d], pb[u], acc[d]);
+  };
+  // Online softmax of one tile; returns the factor O must be rescaled by.
+  auto softmax = [&](f32x16* sacc, bool masked, int k0, V8* pb) -> float {
+    if (masked) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 32 * t + 16 * (r >> 3) + 8 * half + (r & 7);
+          if (key > qi) sacc[t][r] = -INFINITY;
+        }
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
+    mx = half_swap_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+    m_run = m_new;
+    const float mc = m_new * c;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = u >> 1;
+      const int rb = (u & 1) * 8;
+      V8 pk;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        V2 pair;
+        pair[0] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[t][rb + e], c, -mc));
+        pair[1] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[t][rb + e + 1], c, -mc));
+        lsum = dot2_sum(pair, lsum);
+        pk[e] = pair[0];
+        pk[e + 1] = pair[1];
+      }
+      pb[u] = pk;
+    }
+    l_run = fmaf(l_run, alpha, lsum);
+    // Tie the rescale decision to the end of the softmax: without this the
+    // compiler hoists the (rare) rescale branch above the exponentials, which
+    // splits the iteration into blocks and stops MFMA/VALU interleaving.
+    float gated = alpha;
+    asm volatile("" : "+v"(gated) : "v"(l_run));
+    return gated;
+  };
+  auto rescale = [&](float alpha) {
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[d][r] *= alpha;
+    }
+  };
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int j = 0; j <= n_tiles; ++j) {
+    const bool has_next = j + 1 < n_tiles;
+    if (has_next) load_tile(j + 1);
+    const bool do_s = j < w_tiles;
+    const bool do_pv = j >= 1 && j - 1 < w_tiles;
+    if (do_s && do_pv && j < j_mask) {
+      f32x16 sacc[2];
+      V8 pb_new[4];
+      scores(j, sacc);
+      pv(j - 1, pb_prev);
+      const float alpha = softmax(sacc, false, j * kBlockN, pb_new);
+      rescale(alpha);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pb_prev[u] = pb_new[u];
+    } else {
+      f32x16 sacc[2];
+      if (do_s) scores(j, sacc);
+      if (do_pv) pv(j - 1, pb_prev);
+      if (do_s) {
+        const float alpha = softmax(sacc, j >= j_mask, j * kBlockN, pb_prev);
+        rescale(alpha);
+      }
+    }
+    if (has_next) {
+      store_tile(j + 1);
+      __syncthreads();
+    }
+  }
+
+  const float l_tot = half_swap_sum(l_run);
+  if (qi < S) {
+    const float inv = 1.0f / l_tot;
+    T* orow = obase + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        V4 out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = (T)(acc[d][4 * a4 + e] * inv);
+        *reinterpret_cast<V4*>(orow + 32 * d + 8 * a4 + 4 * half) = out;
+      }
+  }
+}
+
 // [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
 // contiguous, zero-filled for keys in [S, S_pad).  One workgroup per 64 keys.
 template <typename T>
@@ -367,15 +625,18 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(
 int64_t padded_seq(int64_t seq_len) { return ceil_div(seq_len, 64) * 64; }
 
 bool launch_supported(int block_m, int block_n, int num_warps, int num_stages) {
-  return (block_m == 128 || block_m == 256) && block_n == kBlockN &&
-         num_warps == kWaves && (num_stages == 1 || num_stages == 2);
+  if (block_n != kBlockN || num_warps != kWaves) return false;
+  if (num_stages == 3) return block_m == 128;  // software-pipelined kernel
+  return (block_m == 128 || block_m == 256) && (num_stages == 1 || num_stages == 2);
 }
 
 template <typename T>
 int launch_attention(const AttnParams& prm, int block_m, int num_stages,
                      hipStream_t stream) {
   const dim3 grid(prm.num_blocks), block(kThreads);
-  if (block_m == 128) {
+  if (num_stages == 3) {
+    hipLaunchKernelGGL((attn_fwd_pipelined_kernel<T>), grid, block, 0, stream, prm);
+  } else if (block_m == 128) {
     if (num_stages == 2)
       hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 2>), grid, block, 0, stream, prm);
     else

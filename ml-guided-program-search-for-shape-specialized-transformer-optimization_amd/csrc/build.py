@@ -38,6 +38,10 @@ HIPCC_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (gfx950 reads/writes C and D from the
+    # unified file); avoids v_accvgpr read/write traffic around VALU updates.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 )
 
 

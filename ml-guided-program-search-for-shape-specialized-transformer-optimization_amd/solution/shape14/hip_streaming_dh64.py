@@ -41,7 +41,7 @@ _DEFAULT_NUM_STAGES = 2
 SUPPORTED_BLOCK_M = frozenset({128, 256})
 SUPPORTED_BLOCK_N = frozenset({64})
 SUPPORTED_NUM_WARPS = frozenset({4})
-SUPPORTED_NUM_STAGES = frozenset({1, 2})
+SUPPORTED_NUM_STAGES = frozenset({1, 2, 3})
 
 
 def launch_config_is_valid(
@@ -53,7 +53,8 @@ def launch_config_is_valid(
     """Whether the launch is one the gfx950 kernel implements.
 
     ``num_warps`` counts 64-wide wavefronts per workgroup and ``num_stages``
-    the number of LDS tile buffers.
+    the number of LDS tile buffers: 1 or 2 select the plain kernel, 3 the
+    software-pipelined one (PV of tile j-1 overlapping the softmax of tile j).
     """
 
     values = (block_m, block_n, num_warps, num_stages)
@@ -64,6 +65,8 @@ def launch_config_is_valid(
         and block_n in SUPPORTED_BLOCK_N
         and num_warps in SUPPORTED_NUM_WARPS
         and num_stages in SUPPORTED_NUM_STAGES
+        # three stages select the software-pipelined kernel (128 query rows)
+        and not (num_stages == 3 and block_m != 128)
     )
 
 

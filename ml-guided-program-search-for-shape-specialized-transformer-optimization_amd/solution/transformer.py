@@ -528,7 +528,15 @@ class UserOptimizedTransformer(nn.Module):
             if value is None
             else tuple(value.shape)
         )
-        signature = (device.type, device.index, dtype, shape, torch.get_float32_matmul_precision())
+        signature = (
+            device.type,
+            device.index,
+            dtype,
+            shape,
+            torch.get_float32_matmul_precision(),
+            self.training,
+            value is not None and torch.is_grad_enabled(),
+        )
         if signature == self._deployment_signature:
             return
         context = self._execution_context(value)

@@ -84,7 +84,60 @@ def parity_gate(reference: torch.Tensor, candidate: torch.Tensor, dtype: torch.d
     return official_compare(reference, candidate, rtol=rtol, atol=atol)
 
 
+@dataclass(frozen=True)
+class ModelParity:
+    """End-to-end parity of a 16-bit model output.
+
+    ``candidate`` and ``reference_path`` (the official op order run in the
+    same 16-bit dtype) are both compared with ``exact`` (the same forward in
+    fp32 from the same rounded weights and inputs).  The candidate passes when
+    it is no less accurate than the reference path, up to the run-to-run
+    spread of two 16-bit pipelines: max-abs within 1.25x of the reference
+    path's (or within the 2e-2 gate), mean-abs within 1.25x (+1e-4), and at
+    most 1.25x as many elements outside the elementwise 2e-2 / 1e-2 gate
+    (+1e-4 of the elements).
+    A strict elementwise gate between two 16-bit pipelines is below the noise
+    floor: a one-ulp rounding flip of a residual-stream value of magnitude
+    4-8 is 0.03-0.06 before the final LayerNorm.
+    """
+
+    candidate: Comparison
+    reference_path: Comparison
+    candidate_vs_reference_path: Comparison
+
+    @property
+    def passed(self) -> bool:
+        c, r = self.candidate, self.reference_path
+        return (
+            c.max_abs_error <= max(BF16_ATOL, 1.25 * r.max_abs_error)
+            and c.mean_abs_error <= 1.25 * r.mean_abs_error + 1e-4
+            and c.failed_elements <= 1.25 * r.failed_elements + 1e-4 * c.total_elements
+        )
+
+    def summary(self) -> str:
+        c, r, x = self.candidate, self.reference_path, self.candidate_vs_reference_path
+        return (
+            f"vs fp32: candidate max_abs={c.max_abs_error:.4g} mean_abs={c.mean_abs_error:.3g} "
+            f"gate_failures={c.failed_elements}/{c.total_elements}; reference path max_abs="
+            f"{r.max_abs_error:.4g} mean_abs={r.mean_abs_error:.3g} gate_failures={r.failed_elements}; "
+            f"candidate vs reference path max_abs={x.max_abs_error:.4g} gate_failures={x.failed_elements}"
+        )
+
+
+def model_parity(
+    exact: torch.Tensor, reference_path: torch.Tensor, candidate: torch.Tensor
+) -> ModelParity:
+    atol, rtol = BF16_ATOL, BF16_RTOL
+    return ModelParity(
+        candidate=official_compare(exact, candidate, rtol=rtol, atol=atol),
+        reference_path=official_compare(exact, reference_path, rtol=rtol, atol=atol),
+        candidate_vs_reference_path=official_compare(reference_path, candidate, rtol=rtol, atol=atol),
+    )
+
+
 __all__ = [
+    "ModelParity",
+    "model_parity",
     "BF16_ATOL",
     "BF16_RTOL",
     "Comparison",
