@@ -16,14 +16,30 @@ launch stream around every attention launch inside the timed region.
 ``cpu_baseline`` times the CPU oracle (fp32 official order, query-blocked
 attention) on a bounded sample of the same workload and scales it to one
 full forward.
+
+``roofline.traffic`` is the attention kernel's HBM bytes per launch measured
+by rocprofv3 PMC counters (FETCH_SIZE and WRITE_SIZE, each scaled by what
+the counter reads for a copy of known size).  Those runs use
+``--kernel attention`` and ``--kernel copy`` below; their result is kept in
+profiles/attn_fwd_c5_chunk_traffic.md as ``key = value`` lines and is
+reported only while ``source_digest`` there equals the digest of the current
+attention source and default launch (otherwise null).
+
+``--kernel attention|norm|copy`` runs one kernel alone at the workload's
+per-chunk shape (for rocprofv3 runs) and prints each launch's duration:
+attention over a packed [2, S, 3D] QKV view exactly as the model hands it
+over, the fused residual+LayerNorm at one chunk's block boundary, or a
+1 GiB device copy used to calibrate the memory counters.
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -226,6 +242,87 @@ def gpu_benchmark(steps: int, warmup: int) -> dict:
     }
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "attn_fwd_c5_chunk_traffic.md"
+ATTENTION_SOURCE = PACKAGE_DIR / "csrc" / "attention_fwd.hip"
+
+
+def attention_source_digest() -> str:
+    """Digest of what the traffic figure depends on: the attention kernel
+    source and the default launch the model uses."""
+
+    from solution.config import HIP_DEFAULT_ATTENTION_LAUNCH
+
+    digest = hashlib.sha256(ATTENTION_SOURCE.read_bytes())
+    digest.update(repr(HIP_DEFAULT_ATTENTION_LAUNCH).encode())
+    return digest.hexdigest()[:16]
+
+
+def measured_traffic() -> float | None:
+    """HBM bytes per attention launch from the committed PMC summary, or None
+    when it is absent or was measured on other kernel source."""
+
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    fields = dict(re.findall(r"^(\w+) = (\S+)\s*$", text, flags=re.MULTILINE))
+    if fields.get("source_digest") != attention_source_digest():
+        log("traffic profile is for other attention source; roofline.traffic = null")
+        return None
+    try:
+        return float(fields["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def kernel_alone(kind: str, repeat: int) -> int:
+    """Run one kernel alone at the workload's per-chunk shape; print the
+    HIP-event duration of every launch."""
+
+    import torch
+
+    from solution.kernels.hip import load_library
+    from solution.kernels.norm import hip_residual
+    from solution.shape14 import hip_streaming_dh64
+
+    load_library()
+    device = torch.device("cuda", 0)
+    w = WORKLOAD
+    batch, seq, width, heads = w["microbatch"], w["seq_len"], w["d_model"], w["heads"]
+    generator = torch.Generator(device=device).manual_seed(7)
+    with torch.inference_mode():
+        if kind == "attention":
+            packed = torch.randn(batch, seq, 3 * width, generator=generator, device=device,
+                                 dtype=torch.bfloat16)
+            q, k, v = (t.transpose(1, 2) for t in packed.unflatten(-1, (3, heads, width // heads)).unbind(dim=2))
+            scale = 1.0 / math.sqrt(width // heads)
+            run = lambda: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(q, k, v, scale=scale)
+            work = f"{_attention_flops(q) / 1e12:.3f} TFLOP per launch"
+        elif kind == "norm":
+            value = torch.randn(batch * seq, width, generator=generator, device=device, dtype=torch.bfloat16)
+            update = torch.randn_like(value)
+            layer_norm = torch.nn.LayerNorm(width).to(device=device, dtype=torch.bfloat16)
+            run = lambda: hip_residual.hip_residual_layer_norm(value, update, layer_norm)
+            work = f"{_norm_bytes(value, update, layer_norm.weight, layer_norm.bias, 1e-5, torch.bfloat16) / 1e9:.4f} GB per launch"
+        elif kind == "copy":
+            source = torch.randn(2**29, generator=generator, device=device, dtype=torch.bfloat16)
+            target = torch.empty_like(source)
+            run = lambda: target.copy_(source)
+            work = "1 GiB read + 1 GiB written per launch"
+        else:
+            raise SystemExit(f"unknown kernel {kind!r}")
+        torch.cuda.synchronize()
+        for index in range(repeat):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            run()
+            end.record()
+            torch.cuda.synchronize()
+            print(f"{kind} launch {index + 1}/{repeat}: {start.elapsed_time(end):.3f} ms ({work})", flush=True)
+    return 0
+
+
 def cpu_baseline() -> dict:
     """Time the CPU oracle on a bounded sample and scale to one full forward.
 
@@ -245,7 +342,7 @@ def cpu_baseline() -> dict:
     threads = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(threads)
     w = WORKLOAD
-    lengths = (2048, 4096, 8192)
+    lengths = (4096, 8192, 16384, 24576)
     times = []
     with torch.inference_mode():
         for seq in lengths:
@@ -281,6 +378,9 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--kernel", choices=("attention", "norm", "copy"),
+                        help="run one kernel alone at the per-chunk shape (profiling)")
+    parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -292,12 +392,15 @@ def main() -> int:
         return 2
     if args.steps <= 0 or args.warmup < 0:
         raise SystemExit("--steps must be positive and --warmup non-negative")
+    if args.kernel is not None:
+        return kernel_alone(args.kernel, max(1, args.repeat))
 
     gpu = gpu_benchmark(args.steps, args.warmup)
     baseline = None if args.no_cpu_baseline else cpu_baseline()
     if baseline is not None:
         log(f"cpu baseline: {baseline['value'] / 1e3:.0f} s per forward on {baseline['cores']} threads")
     achieved = gpu["attention_tflops"]
+    traffic = measured_traffic()
     record = {
         "metric": METRIC,
         "value": round(gpu["ms_per_step"], 3),
@@ -345,7 +448,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "cpu_baseline": baseline,
     }
