@@ -21,7 +21,7 @@ Modules and the reference code each function follows:
 * :mod:`oracle.workload` -- FLOP and byte models
   (benchmarking/shape14_measure.py:36-46) and the BASELINE configurations.
 
-Pinning (tests/test_oracle_*.py): every function is checked against at least
+Pinning (tests/test_oracle.py): every function is checked against at least
 one of the reference's own known answers, a float64 library routine, a
 brute-force loop on tiny inputs, or an invariant that a plausible mistake
 (dropped term, wrong sign, transposed operand, wrong mask side) violates.
