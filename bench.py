@@ -29,7 +29,8 @@ attention source and default launch (otherwise null).
 per-chunk shape (for rocprofv3 runs) and prints each launch's duration:
 attention over a packed [2, S, 3D] QKV view exactly as the model hands it
 over, the fused residual+LayerNorm at one chunk's block boundary, or a
-1 GiB device copy used to calibrate the memory counters.
+1 GiB device copy used to calibrate the memory counters.  Attention runs with
+the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 """
 
 from __future__ import annotations
@@ -153,10 +154,10 @@ def _norm_bytes(value, update, weight, bias, eps, normalized_dtype, *args, **kwa
 def gpu_benchmark(steps: int, warmup: int) -> dict:
     import torch
 
-    from solution.config import hip_config
     from solution.kernels.hip import load_library
     from solution.kernels.norm import hip_residual
     from solution.shape14 import hip_streaming_dh64
+    from solution.shape14.defaults import hip_streamed_config
     from solution.transformer import UserOptimizedTransformer
 
     load_library()
@@ -166,7 +167,7 @@ def gpu_benchmark(steps: int, warmup: int) -> dict:
     model = UserOptimizedTransformer(config)
     _init_xavier(model, seed=1234)
     model = model.to(device=device, dtype=torch.bfloat16).eval()
-    program = hip_config(microbatch_size=w["microbatch"])
+    program = hip_streamed_config(microbatch_size=w["microbatch"])
     model.configure_execution(config=program)
 
     generator = torch.Generator(device=device).manual_seed(1234)
@@ -248,12 +249,12 @@ ATTENTION_SOURCE = PACKAGE_DIR / "csrc" / "attention_fwd.hip"
 
 def attention_source_digest() -> str:
     """Digest of what the traffic figure depends on: the attention kernel
-    source and the default launch the model uses."""
+    source and the launch the long-sequence program uses."""
 
-    from solution.config import HIP_DEFAULT_ATTENTION_LAUNCH
+    from solution.config import HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
 
     digest = hashlib.sha256(ATTENTION_SOURCE.read_bytes())
-    digest.update(repr(HIP_DEFAULT_ATTENTION_LAUNCH).encode())
+    digest.update(repr(HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).encode())
     return digest.hexdigest()[:16]
 
 
@@ -281,6 +282,7 @@ def kernel_alone(kind: str, repeat: int) -> int:
 
     import torch
 
+    from solution.config import HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
     from solution.kernels.hip import load_library
     from solution.kernels.norm import hip_residual
     from solution.shape14 import hip_streaming_dh64
@@ -296,7 +298,10 @@ def kernel_alone(kind: str, repeat: int) -> int:
                                  dtype=torch.bfloat16)
             q, k, v = (t.transpose(1, 2) for t in packed.unflatten(-1, (3, heads, width // heads)).unbind(dim=2))
             scale = 1.0 / math.sqrt(width // heads)
-            run = lambda: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(q, k, v, scale=scale)
+            launch = HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
+            run = lambda: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
+                q, k, v, scale=scale, block_m=launch.block_m, block_n=launch.block_n,
+                num_warps=launch.num_warps, num_stages=launch.num_stages)
             work = f"{_attention_flops(q) / 1e12:.3f} TFLOP per launch"
         elif kind == "norm":
             value = torch.randn(batch * seq, width, generator=generator, device=device, dtype=torch.bfloat16)

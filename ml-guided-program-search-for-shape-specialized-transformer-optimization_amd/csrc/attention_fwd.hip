@@ -7,7 +7,7 @@
 // never materialized, and the result written straight into [B, S, H*64].
 //
 // MI355X formulation (not a translation of the Triton program):
-//  * Each wavefront owns 32*QG query rows; a workgroup is 4 waves (128*QG rows)
+//  * Each wavefront owns 32*QG query rows; a workgroup is 4 or 8 waves
 //    sharing K and V^T tiles of 64 keys staged in LDS (double buffered).
 //  * The score tile is computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_{bf16,f16}: the B operand (Q^T) stays in registers for
@@ -96,12 +96,27 @@ __device__ __forceinline__ u32x4 load8_guarded(const T* src, int64_t first,
   return __builtin_bit_cast(u32x4, v);
 }
 
-template <typename T, int QG, int STAGES>
-__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
+// Cross-half reductions: lanes l and l^32 hold the two key halves of one
+// query row.  v_permlane32_swap exchanges the halves of two registers; the max
+// (or sum) of the two results is the cross-half value in every lane, whichever
+// half each register received.
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T, int QG, int STAGES, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void attn_fwd_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
   typedef typename Vec8<T>::pair_type V2;
-  constexpr int BM = kWaves * 32 * QG;
+  constexpr int BM = WAVES * 32 * QG;
+  constexpr int NT = WAVES * 64;             // threads
+  constexpr int CPT = (kBlockN * 8) / NT;    // 16-byte chunks of a tile per thread
 
   __shared__ __attribute__((aligned(16))) T k_lds[STAGES][kBlockN][kKRow];
   __shared__ __attribute__((aligned(16))) T v_lds[STAGES][kHeadDim][kVRow];
@@ -152,28 +167,39 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     }
   }
 
-  // ---- cooperative tile loader: 2 x 16 B of K and 2 x 16 B of V^T per thread.
-  u32x4 k_pref[2], v_pref[2];
+  // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
+  u32x4 k_pref[CPT], v_pref[CPT];
   auto load_tile = [&](int tile) {
     const int k0 = tile * kBlockN;
+    if (k0 + kBlockN <= S) {  // tile-uniform: every key of the tile exists
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int chunk = tid + kThreads * i;
-      const int row = chunk >> 3;
-      const int c8 = (chunk & 7) * 8;
-      const int key = k0 + row;
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
-      k_pref[i] = raw;
-      // V^T: row = head-dim index, 8 consecutive keys.
-      v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
-                                   (int64_t)k0 + c8, S);
+      for (int i = 0; i < CPT; ++i) {
+        const int chunk = tid + NT * i;
+        const int row = chunk >> 3;
+        const int c8 = (chunk & 7) * 8;
+        k_pref[i] = load16(kbase + (int64_t)(k0 + row) * p.k_ss + c8);
+        v_pref[i] = load16(vbase + (int64_t)row * p.v_sd + k0 + c8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int chunk = tid + NT * i;
+        const int row = chunk >> 3;
+        const int c8 = (chunk & 7) * 8;
+        const int key = k0 + row;
+        u32x4 raw = {0u, 0u, 0u, 0u};
+        if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
+        k_pref[i] = raw;
+        // V^T: row = head-dim index, 8 consecutive keys.
+        v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
+                                     (int64_t)k0 + c8, S);
+      }
     }
   };
   auto store_tile = [&](int stage) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int chunk = tid + kThreads * i;
+    for (int i = 0; i < CPT; ++i) {
+      const int chunk = tid + NT * i;
       const int row = chunk >> 3;
       const int c8 = (chunk & 7) * 8;
       *reinterpret_cast<u32x4*>(&k_lds[stage][row][c8]) = k_pref[i];
@@ -249,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = half_swap_max(mx);
         const float m_new = fmaxf(m_run[g], mx);
         if (__any(m_new > m_run[g])) {
           const float alpha = exp2f((m_run[g] - m_new) * c);
@@ -307,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
     const int qi = wq0 + 32 * g + l32;
-    const float l_tot = l_run[g] + __shfl_xor(l_run[g], 32);
+    const float l_tot = half_swap_sum(l_run[g]);
     if (qi >= S) continue;
     const float inv = 1.0f / l_tot;
     T* orow = obase + (int64_t)qi * p.o_ss;
@@ -323,39 +349,42 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
-// Cross-half reductions: lanes l and l^32 hold the two key halves of one
-// query row.  v_permlane32_swap exchanges the halves of two registers; the max
-// (or sum) of the two results is the cross-half value in every lane, whichever
-// half each register received.
-__device__ __forceinline__ float half_swap_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float half_swap_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
-// Software-pipelined variant (num_stages == 3).  Iteration j computes
-// S^T(j) and its softmax while the PV product of tile j-1 runs on the MFMA
-// pipe: P(j-1) stays in registers for one iteration, V^T tiles are kept in
-// three LDS stages (tile j-1 is still read while tile j+1 is being written)
-// and K tiles in two.  Every PV term is accumulated at the scale of the
-// running maximum it was computed with; the rescale of O by exp(m_old - m_new)
-// is applied at the end of the iteration, after PV(j-1), and skipped when no
-// row of the wave raised its maximum.  Full, unmasked tiles run a body with no
-// branches between the two MFMA groups and the softmax, so the compiler can
-// interleave MFMA and VALU; the first/last tiles of a wave and the diagonal
-// tiles take a general body.  Full tiles load without per-element guards.
-template <typename T>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_pipelined_kernel(AttnParams p) {
+// Software-pipelined variant (num_stages == 3): the score MFMAs of the next
+// tile run while the current tile's exponentials are on the VALU, and the PV
+// MFMAs of the current tile run while the next tile's row maximum is formed.
+// Measured on gfx950, VALU work hides under MFMA execution far better when the
+// same wavefront interleaves the two than when another wavefront on the SIMD
+// supplies it, so the overlap is built into each wavefront's instruction
+// stream rather than left to occupancy.
+//
+// Iteration j of a wave (tiles 0..w_tiles-1), with S^T(j) already scaled and
+// shifted in registers (s * c - m_j * c, masked entries -inf):
+//   phase A: MFMA S^T(j+1) = K(j+1) Q^T       ||  P(j) = exp2(S^T(j)), pack,
+//                                                  row sum
+//   phase B: MFMA O^T += V^T(j) P^T(j)          ||  mask S^T(j+1) if diagonal,
+//                                                  row max, m_{j+1}, shift
+//                                                  S^T(j+1) by m_{j+1}
+//   then, only if some row raised its maximum, O and l are rescaled by
+//   exp2((m_j - m_{j+1}) c) (after PV(j), which was computed at m_j).
+// Two score buffers alternate (the loop is unrolled by two so that no
+// register copies are needed).  The workgroup-level loop keeps K(j+1) and
+// V(j) in LDS during iteration j (two stages each) and prefetches K(j+2) and
+// V(j+1) through registers, with one barrier per iteration.
+//
+// QG query groups of 32 rows per wave would share every K and V^T fragment
+// read from LDS; only QG = 1 is launched: with two groups the double-buffered
+// scores need more registers than two waves per SIMD allow, and at one wave
+// per SIMD the kernel measured slower than the plain 64-row kernel.
+template <typename T, int QG>
+__global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
   typedef typename Vec8<T>::pair_type V2;
-  constexpr int BM = kWaves * 32;
+  constexpr int BM = kWaves * 32 * QG;
 
   __shared__ __attribute__((aligned(16))) T k_lds[2][kBlockN][kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[3][kHeadDim][kVRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[2][kHeadDim][kVRow];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -383,121 +412,133 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_pipelined_kernel(AttnPar
   T* obase = static_cast<T*>(p.o) + b * p.o_sb + (int64_t)h * kHeadDim;
 
   const int q0 = q_tile * BM;
-  const int wq0 = q0 + wave * 32;
-  const int wq_last = (wq0 < S) ? min(wq0 + 32, S) - 1 : -1;
+  const int wq0 = q0 + wave * 32 * QG;
+  const int wq_last = (wq0 < S) ? min(wq0 + 32 * QG, S) - 1 : -1;
   const int key_end = min(q0 + BM, S);
   const int n_tiles = (key_end + kBlockN - 1) / kBlockN;
   // Tiles this wave computes: [0, w_tiles); tiles from j_mask on need the mask.
   const int w_tiles = wq_last < 0 ? 0 : wq_last / kBlockN + 1;
-  const int j_mask = wq0 / kBlockN;  // first tile with a key above some row of the wave
-  const int qi = wq0 + l32;
+  const int j_mask = wq0 / kBlockN;
 
-  V8 qop[4];
+  V8 qop[QG][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
-    qop[s] = __builtin_bit_cast(V8, raw);
+  for (int g = 0; g < QG; ++g) {
+    const int qi = wq0 + 32 * g + l32;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
+      qop[g][s] = __builtin_bit_cast(V8, raw);
+    }
   }
 
+  // ---- cooperative loads: 2 x 16 B of a K tile / a V^T tile per thread.
   u32x4 k_pref[2], v_pref[2];
-  auto load_tile = [&](int tile) {
+  auto load_k = [&](int tile) {
     const int k0 = tile * kBlockN;
-    if (k0 + kBlockN <= S) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int chunk = tid + kThreads * i;
-        const int row = chunk >> 3;
-        const int c8 = (chunk & 7) * 8;
-        k_pref[i] = load16(kbase + (int64_t)(k0 + row) * p.k_ss + c8);
-        v_pref[i] = load16(vbase + (int64_t)row * p.v_sd + k0 + c8);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int chunk = tid + kThreads * i;
-        const int row = chunk >> 3;
-        const int c8 = (chunk & 7) * 8;
-        const int key = k0 + row;
-        u32x4 raw = {0u, 0u, 0u, 0u};
-        if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
-        k_pref[i] = raw;
-        v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
-                                     (int64_t)k0 + c8, S);
-      }
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      const int key = k0 + (chunk >> 3);
+      const int c8 = (chunk & 7) * 8;
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
+      k_pref[i] = raw;
     }
   };
-  auto store_tile = [&](int tile) {
+  auto load_v = [&](int tile) {
+    const int k0 = tile * kBlockN;
+    const bool full = k0 + kBlockN <= S;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int chunk = tid + kThreads * i;
       const int row = chunk >> 3;
       const int c8 = (chunk & 7) * 8;
-      *reinterpret_cast<u32x4*>(&k_lds[tile & 1][row][c8]) = k_pref[i];
-      *reinterpret_cast<u32x4*>(&v_lds[tile % 3][row][c8]) = v_pref[i];
+      const T* src = vbase + (int64_t)row * p.v_sd + k0 + c8;
+      v_pref[i] = full ? load16(src) : load8_guarded<T>(src, (int64_t)k0 + c8, S);
+    }
+  };
+  auto store_k = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      *reinterpret_cast<u32x4*>(&k_lds[tile & 1][chunk >> 3][(chunk & 7) * 8]) = k_pref[i];
+    }
+  };
+  auto store_v = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + kThreads * i;
+      *reinterpret_cast<u32x4*>(&v_lds[tile & 1][chunk >> 3][(chunk & 7) * 8]) = v_pref[i];
     }
   };
 
-  f32x16 acc[2];
+  f32x16 acc[QG][2];
 #pragma unroll
-  for (int d = 0; d < 2; ++d)
+  for (int g = 0; g < QG; ++g)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[d][r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][d][r] = 0.0f;
+  float m_run[QG], l_run[QG];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+  }
   const float c = p.c;
   const int a_row = k_row_for(l32);
-  V8 pb_prev[4];
 
-  // S^T(j) = K(j) Q^T: all eight A operands are read from LDS before the MFMAs.
-  auto scores = [&](int j, f32x16* sacc) {
-    V8 ka[4][2];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        ka[s][t] = *reinterpret_cast<const V8*>(&k_lds[j & 1][32 * t + a_row][16 * s + 8 * half]);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) sacc[t] = mfma32(ka[0][t], qop[0], f32x16{});
-#pragma unroll
-    for (int s = 1; s < 4; ++s)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) sacc[t] = mfma32(ka[s][t], qop[s], sacc[t]);
-  };
-  // O^T += V^T(j) P^T(j).
-  auto pv = [&](int j, const V8* pb) {
-    const int vs = j % 3;
-    V8 va[4][2];
+  // S^T(j) = K(j) Q^T (raw scores) for every group; each K fragment feeds QG MFMAs.
+  auto scores = [&](int j, f32x16 (*s)[2]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int d = 0; d < 2; ++d)
-        va[u][d] = *reinterpret_cast<const V8*>(&v_lds[vs][32 * d + l32][16 * u + 8 * half]);
+      for (int t = 0; t < 2; ++t) {
+        const V8 ka =
+            *reinterpret_cast<const V8*>(&k_lds[j & 1][32 * t + a_row][16 * u + 8 * half]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int d = 0; d < 2; ++d) acc[d] = mfma32(va[u][d], pb[u], acc[d]);
+        for (int g = 0; g < QG; ++g)
+          s[g][t] = mfma32(ka, qop[g][u], u == 0 ? f32x16{} : s[g][t]);
+      }
   };
-  // Online softmax of one tile; returns the factor O must be rescaled by.
-  auto softmax = [&](f32x16* sacc, bool masked, int k0, V8* pb) -> float {
-    if (masked) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 32 * t + 16 * (r >> 3) + 8 * half + (r & 7);
-          if (key > qi) sacc[t][r] = -INFINITY;
-        }
-    }
-    float mx = sacc[0][0];
+  // Keys above the lane's query row of group g -> -inf.
+  auto mask = [&](f32x16* s, int g, int k0) {
+    const int qi = wq0 + 32 * g + l32;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
-    mx = half_swap_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
-    m_run = m_new;
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 32 * t + 16 * (r >> 3) + 8 * half + (r & 7);
+        if (key > qi) s[t][r] = -INFINITY;
+      }
+  };
+  // Row maximum of raw scores (four independent partial maxima), new running
+  // max, and the in-place shift s -> s * c - m_new * c.  Returns
+  // exp2((m_old - m_new) c).
+  auto shift = [&](f32x16* s, int g) -> float {
+    float pm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int t = q >> 1, rb = (q & 1) * 8;
+      pm[q] = s[t][rb];
+#pragma unroll
+      for (int r = 1; r < 8; ++r) pm[q] = fmaxf(pm[q], s[t][rb + r]);
+    }
+    const float mx = half_swap_max(fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3])));
+    const float m_new = fmaxf(m_run[g], mx);
+    const float alpha = __builtin_amdgcn_exp2f((m_run[g] - m_new) * c);
+    m_run[g] = m_new;
     const float mc = m_new * c;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = fmaf(s[t][r], c, -mc);
+    return alpha;
+  };
+  // P(j) = exp2 of the shifted scores, rounded to T and packed as the B
+  // operand of the PV MFMA; returns the row sum of the rounded values.
+  auto exponentiate = [&](const f32x16* s, V8* pb) -> float {
     float lsum = 0.0f;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -507,66 +548,135 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_pipelined_kernel(AttnPar
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         V2 pair;
-        pair[0] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[t][rb + e], c, -mc));
-        pair[1] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[t][rb + e + 1], c, -mc));
+        pair[0] = (T)__builtin_amdgcn_exp2f(s[t][rb + e]);
+        pair[1] = (T)__builtin_amdgcn_exp2f(s[t][rb + e + 1]);
         lsum = dot2_sum(pair, lsum);
         pk[e] = pair[0];
         pk[e + 1] = pair[1];
       }
       pb[u] = pk;
     }
-    l_run = fmaf(l_run, alpha, lsum);
-    // Tie the rescale decision to the end of the softmax: without this the
-    // compiler hoists the (rare) rescale branch above the exponentials, which
-    // splits the iteration into blocks and stops MFMA/VALU interleaving.
-    float gated = alpha;
-    asm volatile("" : "+v"(gated) : "v"(l_run));
-    return gated;
+    return lsum;
   };
-  auto rescale = [&](float alpha) {
+  // O^T += V^T(j) P^T(j) for every group; each V^T fragment feeds QG MFMAs.
+  auto pv = [&](int j, V8 (*pb)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const V8 va =
+            *reinterpret_cast<const V8*>(&v_lds[j & 1][32 * d + l32][16 * u + 8 * half]);
+#pragma unroll
+        for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(va, pb[g][u], acc[g][d]);
+      }
+  };
+  auto rescale = [&](float alpha, int g) {
+    l_run[g] *= alpha;
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int d = 0; d < 2; ++d)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[d][r] *= alpha;
+        for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
     }
   };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int j = 0; j <= n_tiles; ++j) {
-    const bool has_next = j + 1 < n_tiles;
-    if (has_next) load_tile(j + 1);
-    const bool do_s = j < w_tiles;
-    const bool do_pv = j >= 1 && j - 1 < w_tiles;
-    if (do_s && do_pv && j < j_mask) {
-      f32x16 sacc[2];
-      V8 pb_new[4];
-      scores(j, sacc);
-      pv(j - 1, pb_prev);
-      const float alpha = softmax(sacc, false, j * kBlockN, pb_new);
-      rescale(alpha);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pb_prev[u] = pb_new[u];
-    } else {
-      f32x16 sacc[2];
-      if (do_s) scores(j, sacc);
-      if (do_pv) pv(j - 1, pb_prev);
-      if (do_s) {
-        const float alpha = softmax(sacc, j >= j_mask, j * kBlockN, pb_prev);
-        rescale(alpha);
-      }
-    }
-    if (has_next) {
-      store_tile(j + 1);
+  // Workgroup-level end of iteration j: K(j+2) and V(j+1) go from the
+  // prefetch registers into the stages that held K(j) and V(j-1).
+  auto advance = [&](int j) {
+    const bool v_next = j + 1 < n_tiles;
+    if (j + 2 < n_tiles) store_k(j + 2);
+    if (v_next) {
+      store_v(j + 1);
       __syncthreads();
     }
+  };
+  auto prefetch = [&](int j) {
+    if (j + 2 < n_tiles) load_k(j + 2);
+    if (j + 1 < n_tiles) load_v(j + 1);
+  };
+  // Steady-state iteration (tiles j and j+1 both unmasked for every wave):
+  // no branch between the MFMA groups and the VALU work they overlap.
+  auto steady = [&](int j, f32x16 (*cur)[2], f32x16 (*nxt)[2]) {
+    prefetch(j);
+    V8 pb[QG][4];
+    scores(j + 1, nxt);
+#pragma unroll
+    for (int g = 0; g < QG; ++g) l_run[g] += exponentiate(cur[g], pb[g]);
+    pv(j, pb);
+    float alpha[QG];
+#pragma unroll
+    for (int g = 0; g < QG; ++g) alpha[g] = shift(nxt[g], g);
+#pragma unroll
+    for (int g = 0; g < QG; ++g) rescale(alpha[g], g);
+    advance(j);
+  };
+
+  // ---- prologue: K(0), K(1), V(0) in LDS; S^T(0) shifted.
+  load_k(0);
+  store_k(0);
+  if (n_tiles > 1) load_k(1);
+  load_v(0);
+  if (n_tiles > 1) store_k(1);
+  store_v(0);
+  __syncthreads();
+
+  // Every wave forms S^T(0), also one without rows (zero queries): the
+  // steady iterations below run on all four waves.
+  f32x16 s_a[QG][2], s_b[QG][2];
+  scores(0, s_a);
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    if (j_mask == 0) mask(s_a[g], g, 0);
+    (void)shift(s_a[g], g);  // m_run was -inf: nothing to rescale
+  }
+  // Stage 0 of K is rewritten (with K(2)) at the end of iteration 0: every
+  // wave must have read K(0) first.
+  __syncthreads();
+
+  // Iterations [0, j_steady) are steady for all four waves: the workgroup's
+  // first diagonal tile is q0 / 64 and every wave computes at least up to it.
+  // Waves without rows (past the sequence end) run them on zero queries and
+  // write nothing.
+  const int j_steady = max(q0 / kBlockN - 1, 0);
+  int j = 0;
+  for (; j + 1 < j_steady; j += 2) {
+    steady(j, s_a, s_b);
+    steady(j + 1, s_b, s_a);
+  }
+  if (j < j_steady) {
+    steady(j, s_a, s_b);
+#pragma unroll
+    for (int g = 0; g < QG; ++g)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) s_a[g][t] = s_b[g][t];
+    ++j;
+  }
+  // Remaining iterations (diagonal tiles, ragged end): not pipelined; tile j+1
+  // is computed into the same buffer after P(j) has been formed.
+  for (; j < n_tiles; ++j) {
+    prefetch(j);
+    if (j < w_tiles) {
+      V8 pb[QG][4];
+#pragma unroll
+      for (int g = 0; g < QG; ++g) l_run[g] += exponentiate(s_a[g], pb[g]);
+      pv(j, pb);
+      if (j + 1 < w_tiles) {
+        scores(j + 1, s_a);
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+          if (j + 1 >= j_mask) mask(s_a[g], g, (j + 1) * kBlockN);
+          rescale(shift(s_a[g], g), g);
+        }
+      }
+    }
+    advance(j);
   }
 
-  const float l_tot = half_swap_sum(l_run);
-  if (qi < S) {
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    const int qi = wq0 + 32 * g + l32;
+    const float l_tot = half_swap_sum(l_run[g]);
+    if (qi >= S) continue;
     const float inv = 1.0f / l_tot;
     T* orow = obase + (int64_t)qi * p.o_ss;
 #pragma unroll
@@ -575,7 +685,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_pipelined_kernel(AttnPar
       for (int a4 = 0; a4 < 4; ++a4) {
         V4 out;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) out[e] = (T)(acc[d][4 * a4 + e] * inv);
+        for (int e = 0; e < 4; ++e) out[e] = (T)(acc[g][d][4 * a4 + e] * inv);
         *reinterpret_cast<V4*>(orow + 32 * d + 8 * a4 + 4 * half) = out;
       }
   }
@@ -625,27 +735,41 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(
 int64_t padded_seq(int64_t seq_len) { return ceil_div(seq_len, 64) * 64; }
 
 bool launch_supported(int block_m, int block_n, int num_warps, int num_stages) {
-  if (block_n != kBlockN || num_warps != kWaves) return false;
-  if (num_stages == 3) return block_m == 128;  // software-pipelined kernel
-  return (block_m == 128 || block_m == 256) && (num_stages == 1 || num_stages == 2);
+  if (block_n != kBlockN || (num_warps != 4 && num_warps != 8)) return false;
+  if (num_stages == 3) return block_m == 128 && num_warps == 4;  // software-pipelined kernel
+  if (num_stages != 1 && num_stages != 2) return false;
+  // 32 or 64 query rows per wave.
+  return block_m == 32 * num_warps || block_m == 64 * num_warps;
+}
+
+template <typename T, int WAVES>
+void launch_plain(const AttnParams& prm, int qg, int num_stages, hipStream_t stream) {
+  const dim3 grid(prm.num_blocks), block(WAVES * 64);
+  if (qg == 1) {
+    if (num_stages == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 2, WAVES>), grid, block, 0, stream, prm);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 1, WAVES>), grid, block, 0, stream, prm);
+  } else {
+    if (num_stages == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 2, WAVES>), grid, block, 0, stream, prm);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 1, WAVES>), grid, block, 0, stream, prm);
+  }
 }
 
 template <typename T>
-int launch_attention(const AttnParams& prm, int block_m, int num_stages,
+int launch_attention(const AttnParams& prm, int block_m, int num_warps, int num_stages,
                      hipStream_t stream) {
-  const dim3 grid(prm.num_blocks), block(kThreads);
   if (num_stages == 3) {
-    hipLaunchKernelGGL((attn_fwd_pipelined_kernel<T>), grid, block, 0, stream, prm);
-  } else if (block_m == 128) {
-    if (num_stages == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 2>), grid, block, 0, stream, prm);
-    else
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 1>), grid, block, 0, stream, prm);
+    hipLaunchKernelGGL((attn_fwd_pipelined_kernel<T, 1>), dim3(prm.num_blocks), dim3(kThreads), 0,
+                       stream, prm);
   } else {
-    if (num_stages == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 2>), grid, block, 0, stream, prm);
+    const int qg = block_m / (32 * num_warps);
+    if (num_warps == 8)
+      launch_plain<T, 8>(prm, qg, num_stages, stream);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 1>), grid, block, 0, stream, prm);
+      launch_plain<T, 4>(prm, qg, num_stages, stream);
   }
   return check_hip(hipGetLastError(), "attention kernel launch");
 }
@@ -779,6 +903,7 @@ extern "C" int sah_causal_attention_bsd(
     return fail(SAH_ERR_INVALID_ARGUMENT,
                 "value needs a unit stride on the head_dim or the seq axis");
   }
-  return (dtype == SAH_DTYPE_BF16) ? launch_attention<bf16>(prm, block_m, num_stages, stream)
-                                   : launch_attention<f16>(prm, block_m, num_stages, stream);
+  return (dtype == SAH_DTYPE_BF16)
+             ? launch_attention<bf16>(prm, block_m, num_warps, num_stages, stream)
+             : launch_attention<f16>(prm, block_m, num_warps, num_stages, stream);
 }

@@ -635,6 +635,13 @@ def portable_streamed_config(*, microbatch_size: int = 1) -> ConfigSpec:
 HIP_DEFAULT_ATTENTION_LAUNCH = AttentionLaunchParams(
     block_m=128, block_n=64, num_warps=4, num_stages=2
 )
+# Long sequences: 64 query rows per wavefront, so every K and V^T fragment read
+# from LDS feeds two MFMAs and each wave carries four independent accumulation
+# chains.  Short sequences keep 128-row tiles, which give twice as many
+# workgroups to fill 256 CUs.
+HIP_LONG_SEQUENCE_ATTENTION_LAUNCH = AttentionLaunchParams(
+    block_m=256, block_n=64, num_warps=4, num_stages=2
+)
 HIP_DEFAULT_NORM_LAUNCH = NormLaunchParams(block_rows=4, num_warps=4)
 
 
@@ -681,6 +688,7 @@ __all__ = [
     "HIP_ATTENTION_BACKENDS",
     "HIP_DEFAULT_ATTENTION_LAUNCH",
     "HIP_DEFAULT_NORM_LAUNCH",
+    "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",
     "HIP_RESIDUAL_NORM_BACKENDS",
     "LAUNCHED_ATTENTION_BACKENDS",
     "TRITON_ATTENTION_BACKENDS",

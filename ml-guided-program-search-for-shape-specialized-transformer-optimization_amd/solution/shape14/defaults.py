@@ -5,13 +5,15 @@ Shape 14 program (solution/shape14/defaults.py:22-49) so its config_id can be
 reproduced; its Triton attention is rejected by this build's PlanBuilder.
 
 hip_streamed_config is the gfx950 program for long sequences: HIP streaming
-attention and HIP norms with ordered microbatches (2 sequences per chunk by
-default, the BASELINE long-sequence configuration).
+attention (64 query rows per wavefront) and HIP norms with ordered
+microbatches (2 sequences per chunk by default, the BASELINE long-sequence
+configuration).
 """
 
 from __future__ import annotations
 
 from solution.config import (
+    HIP_LONG_SEQUENCE_ATTENTION_LAUNCH,
     AttentionBackend,
     AttentionLaunchParams,
     AttentionOutputBridge,
@@ -59,7 +61,9 @@ def conservative_streamed_config() -> ConfigSpec:
 def hip_streamed_config(*, microbatch_size: int = DEFAULT_MICROBATCH_SIZE) -> ConfigSpec:
     """The gfx950 long-sequence program with ordered microbatches."""
 
-    return hip_config(microbatch_size=microbatch_size)
+    return hip_config(
+        microbatch_size=microbatch_size, attention_launch=HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
+    )
 
 
 __all__ = ["DEFAULT_MICROBATCH_SIZE", "conservative_streamed_config", "hip_streamed_config"]

@@ -38,9 +38,9 @@ _DEFAULT_BLOCK_M = 128
 _DEFAULT_BLOCK_N = 64
 _DEFAULT_NUM_WARPS = 4
 _DEFAULT_NUM_STAGES = 2
-SUPPORTED_BLOCK_M = frozenset({128, 256})
+SUPPORTED_BLOCK_M = frozenset({128, 256, 512})
 SUPPORTED_BLOCK_N = frozenset({64})
-SUPPORTED_NUM_WARPS = frozenset({4})
+SUPPORTED_NUM_WARPS = frozenset({4, 8})
 SUPPORTED_NUM_STAGES = frozenset({1, 2, 3})
 
 
@@ -52,9 +52,12 @@ def launch_config_is_valid(
 ) -> bool:
     """Whether the launch is one the gfx950 kernel implements.
 
-    ``num_warps`` counts 64-wide wavefronts per workgroup and ``num_stages``
-    the number of LDS tile buffers: 1 or 2 select the plain kernel, 3 the
-    software-pipelined one (PV of tile j-1 overlapping the softmax of tile j).
+    ``num_warps`` counts 64-wide wavefronts per workgroup (4 or 8) and
+    ``num_stages`` the number of LDS tile buffers: 1 or 2 select the plain
+    kernel, with 32 or 64 query rows per wavefront (``block_m`` = 32 or 64 x
+    ``num_warps``); 3 selects the software-pipelined kernel (4 wavefronts,
+    128 rows), in which the score MFMAs of the next tile overlap the
+    exponentials of the current one.
     """
 
     values = (block_m, block_n, num_warps, num_stages)
@@ -65,8 +68,12 @@ def launch_config_is_valid(
         and block_n in SUPPORTED_BLOCK_N
         and num_warps in SUPPORTED_NUM_WARPS
         and num_stages in SUPPORTED_NUM_STAGES
-        # three stages select the software-pipelined kernel (128 query rows)
-        and not (num_stages == 3 and block_m != 128)
+        and (
+            # three stages select the software-pipelined kernel (4 waves, 128 rows)
+            (block_m == 128 and num_warps == 4)
+            if num_stages == 3
+            else block_m in (32 * num_warps, 64 * num_warps)
+        )
     )
 
 

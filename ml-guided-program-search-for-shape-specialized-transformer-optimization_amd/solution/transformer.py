@@ -507,11 +507,11 @@ class UserOptimizedTransformer(nn.Module):
             if is_gfx950(device):
                 load_library()  # a gfx950 device without the library is an error
                 if streamed:
-                    from .shape14.defaults import DEFAULT_MICROBATCH_SIZE
+                    from .shape14.defaults import DEFAULT_MICROBATCH_SIZE, hip_streamed_config
 
                     batch = int(shape[0])
                     microbatch = DEFAULT_MICROBATCH_SIZE if batch % DEFAULT_MICROBATCH_SIZE == 0 else 1
-                    return hip_config(microbatch_size=microbatch)
+                    return hip_streamed_config(microbatch_size=microbatch)
                 return hip_config()
         return portable_streamed_config() if streamed else portable_config()
 

@@ -61,31 +61,33 @@ def _assert_parity(reference, candidate, dtype, what):
     )
 
 
-LAUNCHES = [(128, 2), (256, 2), (128, 3)]  # (block_m, num_stages); 3 = pipelined kernel
+# (block_m, num_warps, num_stages): 32 or 64 rows per wave, 4 or 8 waves; 3 stages = pipelined kernel
+LAUNCHES = [(128, 4, 2), (256, 4, 2), (256, 8, 2), (512, 8, 2), (512, 8, 1), (128, 4, 3)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("block_m,num_stages", LAUNCHES)
+@pytest.mark.parametrize("block_m,num_warps,num_stages", LAUNCHES)
 @pytest.mark.parametrize(
     "batch,heads,seq",
     [(1, 1, 1), (1, 2, 17), (2, 3, 100), (2, 2, 257), (1, 2, 1000), (3, 1, 130)],
 )
-def test_attention_matches_oracle(gpu_device, dtype, block_m, num_stages, batch, heads, seq):
-    print(f"attention parity dtype={dtype} launch={(block_m, num_stages)} shape={(batch, heads, seq)}", flush=True)
+def test_attention_matches_oracle(gpu_device, dtype, block_m, num_warps, num_stages, batch, heads, seq):
+    launch = (block_m, num_warps, num_stages)
+    print(f"attention parity dtype={dtype} launch={launch} shape={(batch, heads, seq)}", flush=True)
     q, k, v = _inputs(batch, heads, seq, dtype=dtype, seed=seq * 7 + heads)
-    output = _run(q, k, v, gpu_device, block_m=block_m, num_stages=num_stages)
+    output = _run(q, k, v, gpu_device, block_m=block_m, num_warps=num_warps, num_stages=num_stages)
     reference = _to_bsd(_oracle(q, k, v, 1 / 8))
     _assert_parity(reference, output, dtype, f"{dtype} {block_m} {(batch, heads, seq)}")
 
 
-@pytest.mark.parametrize("num_stages", [1, 2, 3])
-def test_baseline_config3_attention(gpu_device, num_stages):
+@pytest.mark.parametrize("block_m,num_warps,num_stages", LAUNCHES)
+def test_baseline_config3_attention(gpu_device, block_m, num_warps, num_stages):
     """B8 H16 S2048 Dh64, inputs N(0,1)/sqrt(64); the op
     applies the 1/sqrt(64) softmax scale on top."""
 
-    print(f"config-3 attention num_stages={num_stages}", flush=True)
+    print(f"config-3 attention launch={(block_m, num_warps, num_stages)}", flush=True)
     q, k, v = _inputs(8, 16, 2048, dtype=torch.bfloat16, seed=1234, scale_inputs=1 / 8)
-    output = _run(q, k, v, gpu_device, block_m=128, num_stages=num_stages)
+    output = _run(q, k, v, gpu_device, block_m=block_m, num_warps=num_warps, num_stages=num_stages)
     reference = _to_bsd(_oracle(q, k, v, 1 / 8))
     _assert_parity(reference, output, torch.bfloat16, "config 3")
 
@@ -96,8 +98,8 @@ def test_launch_shapes_and_stages_are_bitwise_identical(gpu_device):
 
     q, k, v = _inputs(2, 4, 777, dtype=torch.bfloat16, seed=5)
     outputs = [
-        _run(q, k, v, gpu_device, block_m=block_m, num_stages=stages)
-        for block_m in (128, 256)
+        _run(q, k, v, gpu_device, block_m=block_m, num_warps=warps, num_stages=stages)
+        for block_m, warps in ((128, 4), (256, 4), (256, 8), (512, 8))
         for stages in (1, 2)
     ]
     for other in outputs[1:]:
@@ -159,25 +161,29 @@ def test_first_row_copies_first_value(gpu_device):
         assert torch.equal(output[:, 0, head * 64 : (head + 1) * 64], v[:, head, 0])
 
 
-@pytest.mark.parametrize("block_m,num_stages", LAUNCHES)
-def test_batch_slices_are_independent(gpu_device, block_m, num_stages):
+@pytest.mark.parametrize("block_m,num_warps,num_stages", LAUNCHES)
+def test_batch_slices_are_independent(gpu_device, block_m, num_warps, num_stages):
     """Running a sub-batch gives bitwise the rows of the full batch (the
     property the streamed chunk driver relies on)."""
 
+    launch = dict(block_m=block_m, num_warps=num_warps, num_stages=num_stages)
     q, k, v = _inputs(4, 2, 400, dtype=torch.bfloat16, seed=17)
-    full = _run(q, k, v, gpu_device, block_m=block_m, num_stages=num_stages)
-    part = _run(q[1:3], k[1:3], v[1:3], gpu_device, block_m=block_m, num_stages=num_stages)
+    full = _run(q, k, v, gpu_device, **launch)
+    part = _run(q[1:3], k[1:3], v[1:3], gpu_device, **launch)
     assert torch.equal(full[1:3], part)
 
 
-def test_long_sequence_sampled_rows(gpu_device):
+@pytest.mark.parametrize("block_m,num_warps,num_stages", [(128, 4, 3), (256, 4, 2), (512, 8, 2)])
+def test_long_sequence_sampled_rows(gpu_device, block_m, num_warps, num_stages):
     """S = 100000 (the long-sequence configuration's length): sampled rows,
     including the last ones that see every key, against float64 per-row math."""
 
     seq = 100_000
-    print("long-sequence attention S=100000", flush=True)
+    print(f"long-sequence attention S=100000 launch={(block_m, num_warps, num_stages)}", flush=True)
     q, k, v = _inputs(1, 2, seq, dtype=torch.bfloat16, seed=2024)
-    output = _run(q, k, v, gpu_device, block_m=128, num_stages=3).float().cpu()
+    output = _run(
+        q, k, v, gpu_device, block_m=block_m, num_warps=num_warps, num_stages=num_stages
+    ).float().cpu()
     rng = np.random.default_rng(0)
     rows = np.unique(
         np.concatenate([np.arange(0, 40), np.arange(seq - 40, seq), rng.integers(0, seq, 40)])

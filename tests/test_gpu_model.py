@@ -115,14 +115,14 @@ def test_long_sequence_forward_prefix_matches_the_oracle(gpu_device):
     (D1024 H16 F4096 L2, bf16).  Causality makes its first rows a function of
     the prefix only, so they are checked against the oracle on that prefix."""
 
-    from solution.config import hip_config
+    from solution.shape14.defaults import hip_streamed_config
 
     seq, prefix = 100_000, 1024
     config = TransformerConfig(1, seq, 1024, 16, 4096, 2, True)
     state = xavier_init_weights(config, seed=2024)
     x = generate_input(config, seed=2024).to(torch.bfloat16)
     model = _model(config, state, gpu_device, torch.bfloat16)
-    model.configure_execution(config=hip_config(microbatch_size=1))
+    model.configure_execution(config=hip_streamed_config(microbatch_size=1))
     print("long-sequence forward S=100000", flush=True)
     with torch.inference_mode():
         output = model(x.to(gpu_device))

@@ -45,13 +45,18 @@ def test_host_only_entry_points():
     assert library.sah_causal_attention_launch_supported(64, 64, 4, 2) == 0
     assert library.sah_causal_attention_launch_supported(128, 64, 4, 3) == 1
     assert library.sah_causal_attention_launch_supported(256, 64, 4, 3) == 0
+    assert library.sah_causal_attention_launch_supported(512, 64, 8, 2) == 1
+    assert library.sah_causal_attention_launch_supported(512, 64, 4, 2) == 0
+    assert library.sah_causal_attention_launch_supported(128, 64, 8, 3) == 0
     from solution.shape14.hip_streaming_dh64 import launch_config_is_valid
 
-    for block_m in (64, 128, 256):
-        for stages in (1, 2, 3, 4):
-            assert launch_config_is_valid(block_m, 64, 4, stages) == bool(
-                library.sah_causal_attention_launch_supported(block_m, 64, 4, stages)
-            )
+    for block_m in (64, 128, 256, 512, 1024):
+        for block_n in (32, 64, 128):
+            for warps in (2, 4, 8):
+                for stages in (1, 2, 3, 4):
+                    assert launch_config_is_valid(block_m, block_n, warps, stages) == bool(
+                        library.sah_causal_attention_launch_supported(block_m, block_n, warps, stages)
+                    ), (block_m, block_n, warps, stages)
     # V given head_dim-contiguous needs a V^T workspace padded to 64 keys.
     assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 3072, 1, 2) == 2 * 16 * 64 * 100032 * 2
     # seq-contiguous V (a V^T buffer) needs none.

@@ -120,7 +120,9 @@ def test_hip_config_round_trips_and_uses_existing_fields():
     assert payload["program"]["attention"] == "hip_streaming_dh64"
     assert payload["program"]["residual_norm"] == "hip_fused"
     assert payload["program"]["initial_norm"] == "hip"
-    assert config.config_id == hip_streamed_config().config_id
+    streamed = hip_streamed_config()
+    assert streamed.schedule.attention_launch == AttentionLaunchParams(256, 64, 4, 2)
+    assert streamed == hip_config(microbatch_size=2, attention_launch=streamed.schedule.attention_launch)
     assert TritonAttentionParams is AttentionLaunchParams
 
 
