@@ -635,12 +635,13 @@ def portable_streamed_config(*, microbatch_size: int = 1) -> ConfigSpec:
 HIP_DEFAULT_ATTENTION_LAUNCH = AttentionLaunchParams(
     block_m=128, block_n=64, num_warps=4, num_stages=2
 )
-# Long sequences: 64 query rows per wavefront, so every K and V^T fragment read
-# from LDS feeds two MFMAs and each wave carries four independent accumulation
-# chains.  Short sequences keep 128-row tiles, which give twice as many
-# workgroups to fill 256 CUs.
+# Long sequences: 256-row query tiles shared by 8 wavefronts, which halves the
+# K/V^T tile loads, LDS stores and barriers per FLOP against 128-row tiles
+# (measured fastest of the 4/8-wave, 32/64-rows-per-wave launches on the
+# 100k-token chunk).  Short sequences keep 128-row tiles, which give twice as
+# many workgroups to fill 256 CUs.
 HIP_LONG_SEQUENCE_ATTENTION_LAUNCH = AttentionLaunchParams(
-    block_m=256, block_n=64, num_warps=4, num_stages=2
+    block_m=256, block_n=64, num_warps=8, num_stages=2
 )
 HIP_DEFAULT_NORM_LAUNCH = NormLaunchParams(block_rows=4, num_warps=4)
 

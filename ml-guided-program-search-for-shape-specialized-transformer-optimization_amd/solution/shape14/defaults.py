@@ -5,7 +5,7 @@ Shape 14 program (solution/shape14/defaults.py:22-49) so its config_id can be
 reproduced; its Triton attention is rejected by this build's PlanBuilder.
 
 hip_streamed_config is the gfx950 program for long sequences: HIP streaming
-attention (64 query rows per wavefront) and HIP norms with ordered
+attention (256-row tiles over 8 wavefronts) and HIP norms with ordered
 microbatches (2 sequences per chunk by default, the BASELINE long-sequence
 configuration).
 """

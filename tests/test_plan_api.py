@@ -121,7 +121,7 @@ def test_hip_config_round_trips_and_uses_existing_fields():
     assert payload["program"]["residual_norm"] == "hip_fused"
     assert payload["program"]["initial_norm"] == "hip"
     streamed = hip_streamed_config()
-    assert streamed.schedule.attention_launch == AttentionLaunchParams(256, 64, 4, 2)
+    assert streamed.schedule.attention_launch == AttentionLaunchParams(256, 64, 8, 2)
     assert streamed == hip_config(microbatch_size=2, attention_launch=streamed.schedule.attention_launch)
     assert TritonAttentionParams is AttentionLaunchParams
 
