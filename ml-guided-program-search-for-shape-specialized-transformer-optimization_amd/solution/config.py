@@ -649,14 +649,21 @@ HIP_DEFAULT_NORM_LAUNCH = NormLaunchParams(block_rows=4, num_warps=4)
 def hip_config(
     *,
     microbatch_size: int | None = None,
+    graph: bool = False,
     attention_launch: AttentionLaunchParams = HIP_DEFAULT_ATTENTION_LAUNCH,
     norm_launch: NormLaunchParams = HIP_DEFAULT_NORM_LAUNCH,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
     norms and HIP initial norm, projections and FFN in the model dtype on
-    hipBLASLt.  ``microbatch_size`` selects the streamed schedule."""
+    hipBLASLt.  ``microbatch_size`` selects the streamed schedule, ``graph``
+    the graph-replay runtime (one HIP graph per input signature)."""
 
-    runtime = RuntimeBackend.EAGER if microbatch_size is None else RuntimeBackend.STREAMED
+    if graph and microbatch_size is not None:
+        raise ValueError("the graph runtime and the streamed schedule are exclusive")
+    if graph:
+        runtime = RuntimeBackend.CUDA_GRAPH
+    else:
+        runtime = RuntimeBackend.EAGER if microbatch_size is None else RuntimeBackend.STREAMED
     return ConfigSpec(
         program=ProgramConfig(
             attention=AttentionBackend.HIP_STREAMING_DH64,

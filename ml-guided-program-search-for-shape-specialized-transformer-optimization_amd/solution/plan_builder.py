@@ -282,6 +282,8 @@ class PlanBuilder:
             from .shape14.planning import validate_streamed_runtime
 
             return validate_streamed_runtime(config, context, reject)
+        if runtime is RuntimeBackend.CUDA_GRAPH:  # a HIP graph on ROCm
+            return context
         _unavailable(reject, "schedule.runtime", f"the {runtime.value} runtime")
         if runtime is RuntimeBackend.BATCH_TILED_CUDA_GRAPH:
             tile = config.schedule.batch_tile_size

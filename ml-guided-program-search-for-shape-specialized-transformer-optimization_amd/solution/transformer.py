@@ -452,6 +452,7 @@ class UserOptimizedTransformer(nn.Module):
             ]
         )
         self.final_norm = nn.LayerNorm(config.d_model)
+        self._graph_replay: Any = None  # GraphReplay of the cuda_graph runtime
         self._runtime_plan_signature: tuple[object, ...] | None = None
         self._runtime_plan: ExecutionPlan | None = None
         self._execution_observation_enabled = False
@@ -466,6 +467,7 @@ class UserOptimizedTransformer(nn.Module):
 
     # ------------------------------------------------------------ state
     def _invalidate_runtime_state(self) -> None:
+        self._graph_replay = None
         self._runtime_plan_signature = None
         self._runtime_plan = None
         self._last_execution_observation = None
@@ -897,6 +899,17 @@ class UserOptimizedTransformer(nn.Module):
             )
             if self._execution_observation_enabled and self._last_execution_observation is not None:
                 self._last_execution_observation["runtime_backend"] = RuntimeBackend.STREAMED.value
+            return output
+        if plan.use_cuda_graph:
+            if self._graph_replay is None:
+                from .runtimes.graph_replay import GraphReplay
+
+                self._graph_replay = GraphReplay(reuse_unchanged_input=plan.reuse_unchanged_input)
+            output = self._graph_replay.run(
+                lambda value, mask: self._forward_eager(value, mask, plan), x, valid_token_mask
+            )
+            if self._execution_observation_enabled and self._last_execution_observation is not None:
+                self._last_execution_observation["runtime_backend"] = RuntimeBackend.CUDA_GRAPH.value
             return output
         if plan.runtime_backend is not RuntimeBackend.EAGER:
             raise RuntimeError(f"runtime {plan.runtime_backend.value} is not executable here")

@@ -181,6 +181,36 @@ def test_reference_shape14_program_with_hip_kernels_on_an_fp32_model(gpu_device)
     assert observed["residual_norm_backend"] == "hip_mixed" and observed["complete"]
 
 
+def test_graph_runtime_replays_equal_eager_execution(gpu_device):
+    """The graph-replay runtime (a HIP graph per input signature) on the
+    short-sequence configuration's widths: several replays with new inputs,
+    eager work and synchronizations between them, each bitwise equal to the
+    eager program on the same input."""
+
+    from solution.config import hip_config
+
+    config = TransformerConfig(8, 256, 512, 8, 2048, 2, True)
+    state = xavier_init_weights(config, seed=11)
+    graph_model = _model(config, state, gpu_device, torch.bfloat16)
+    graph_model.configure_execution(config=hip_config(graph=True))
+    graph_model.set_execution_observation(True)
+    eager_model = _model(config, state, gpu_device, torch.bfloat16)
+    eager_model.configure_execution(config=hip_config())
+    with torch.inference_mode():
+        for seed in (1, 2, 3, 4):
+            print(f"graph replay input seed {seed}", flush=True)
+            x = generate_input(config, seed=seed).to(torch.bfloat16).to(gpu_device)
+            replayed = graph_model(x)
+            torch.cuda.synchronize()
+            expected = eager_model(x)
+            torch.cuda.synchronize()
+            assert torch.equal(replayed, expected), f"replay {seed} differs from eager"
+        observed = graph_model.describe_execution_path()
+        assert observed["runtime_backend"] == "cuda_graph"
+        with pytest.raises(RuntimeError, match="one static input signature"):
+            graph_model(torch.zeros(4, 256, 512, dtype=torch.bfloat16, device=gpu_device))
+
+
 def test_default_resolution_on_gfx950_selects_the_hip_program(gpu_device):
     from solution.config import hip_config
 

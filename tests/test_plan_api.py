@@ -205,6 +205,23 @@ def test_streamed_microbatch_rules():
     assert ("schedule.runtime", "mask_not_supported") in {(v.field, v.code) for v in masked.violations}
 
 
+def test_graph_runtime_plans_for_inference_on_the_gpu():
+    builder = PlanBuilder()
+    config = hip_config(graph=True)
+    assert config.schedule.runtime is RuntimeBackend.CUDA_GRAPH
+    assert ConfigSpec.from_dict(json.loads(json.dumps(config.to_dict()))) == config
+    short = _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4)
+    plan = builder.build(config, short, _gfx950())
+    assert plan.use_cuda_graph and plan.describe()["runtime_backend"] == "cuda_graph"
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    cpu = builder.evaluate(config, _context(device="cpu"), _gfx950(device_type="cpu", gcn_arch=None))
+    assert ("schedule.runtime", "requires_cuda") in codes(cpu)
+    grad = builder.evaluate(config, _context(grad=True), _gfx950())
+    assert ("schedule.runtime", "requires_inference") in codes(grad)
+    with pytest.raises(ValueError, match="exclusive"):
+        hip_config(graph=True, microbatch_size=2)
+
+
 def test_reference_only_backends_are_unavailable_not_silently_replaced():
     records = json.loads((GOLDEN / "reference_configs.json").read_text())["records"]
     builder = PlanBuilder()
