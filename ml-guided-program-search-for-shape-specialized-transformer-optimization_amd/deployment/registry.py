@@ -100,11 +100,14 @@ def resolve_deployed_config(
     *,
     hardware: EnvironmentFingerprint | dict[str, Any],
     shape: ShapeFingerprint | dict[str, Any],
-    path: str | Path = DEFAULT_DEPLOYED_CONFIGS_PATH,
+    path: str | Path | None = None,
 ) -> ConfigSpec | None:
-    """The exact environment/shape config, or None when never measured."""
+    """The exact environment/shape config, or None when never measured.
+    ``path`` defaults to this module's DEFAULT_DEPLOYED_CONFIGS_PATH, read at
+    call time."""
 
     hardware_key, shape_key = _as_fingerprint(hardware), _as_shape(shape)
+    path = DEFAULT_DEPLOYED_CONFIGS_PATH if path is None else path
     for entry in _matching_entries(hardware=hardware_key, path=path):
         if isinstance(entry.get("shape"), dict) and ShapeFingerprint.from_dict(entry["shape"]) == shape_key:
             return ConfigSpec.from_dict(entry["config"])

@@ -1,0 +1,117 @@
+"""The HIP launch search (autotune/hip_launch_search.py): its space, its
+legality filtering and its publication gate (no GPU needed)."""
+
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+
+from autotune.hip_launch_search import (
+    ATTENTION_LAUNCHES,
+    MICROBATCHES,
+    NORM_LAUNCHES,
+    WORKLOADS,
+    HipLaunchSearch,
+    SearchShape,
+    _runtime_variants,
+    _with_attention,
+    _with_norms,
+    outputs_agree,
+)
+from solution.config import RuntimeBackend, hip_config
+from solution.plan_builder import HardwareCapabilities
+from solution.shape14.defaults import hip_streamed_config
+
+
+def _gfx950() -> HardwareCapabilities:
+    return HardwareCapabilities(
+        device_type="cuda", compute_capability=(9, 5), shared_memory_per_block=65536,
+        mem_efficient_sdp=False, cudnn_sdp=False, cudnn_available=False, torch_compile=False,
+        triton_shape13_attention=False, triton_dh8_attention=False, triton_residual_norm=False,
+        triton_mixed_residual_norm=False, triton_initial_norm=False, triton_exact_gelu=False,
+        triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
+        hip_residual_norm=True, hip_initial_norm=True,
+    )
+
+
+def test_space_is_every_kernel_launch():
+    from solution.kernels.hip import _library
+
+    library = _library.load_library()
+    implemented = {
+        (m, w, s)
+        for m in (64, 128, 256, 512, 1024)
+        for w in (2, 4, 8)
+        for s in (1, 2, 3, 4)
+        if library.sah_causal_attention_launch_supported(m, 64, w, s)
+    }
+    assert {(l.block_m, l.num_warps, l.num_stages) for l in ATTENTION_LAUNCHES} == implemented
+
+
+def test_every_candidate_of_the_long_sequence_space_is_legal():
+    shape = SearchShape(*WORKLOADS["c5"])
+    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
+    assert search.streamed and search.timed == 4
+    device = torch.device("cuda")
+    base = search.incumbent()
+    assert base == hip_streamed_config()
+    for launch in ATTENTION_LAUNCHES:
+        assert search.legal(_with_attention(base, launch), device), launch
+    for launch in NORM_LAUNCHES:
+        assert search.legal(_with_norms(base, launch), device), launch
+    variants = _runtime_variants(base, streamed=True, batch=4)
+    assert [v.schedule.microbatch_size for v in variants] == list(MICROBATCHES)
+    assert all(search.legal(v, device) for v in variants)
+
+
+def test_resident_space_offers_eager_and_graph_replay():
+    shape = SearchShape(*WORKLOADS["c2"])
+    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
+    assert not search.streamed and search.timed == 64 and search.incumbent() == hip_config()
+    variants = _runtime_variants(hip_config(), streamed=False, batch=64)
+    assert [v.schedule.runtime for v in variants] == [RuntimeBackend.EAGER, RuntimeBackend.CUDA_GRAPH]
+    assert all(search.legal(v, torch.device("cuda")) for v in variants)
+    # an attention launch the plan builder rejects is never timed: wrong head count
+    wide = dataclasses.replace(shape, num_heads=4)
+    assert not HipLaunchSearch(torch.nn.Identity(), wide, hardware=_gfx950()).legal(
+        hip_config(), torch.device("cuda")
+    )
+
+
+def test_publication_gate():
+    generator = torch.Generator().manual_seed(0)
+    base = (torch.randn(2, 64, 128, generator=generator) * 3).to(torch.bfloat16)
+    assert outputs_agree(base, base)
+    noisy = base.float().clone()
+    noisy.view(-1)[:10] += 0.0625  # one bf16 ulp at |x| in [8, 16) on a few elements
+    assert outputs_agree(noisy.to(torch.bfloat16), base)
+    wrong = base.float().clone()
+    wrong.view(-1)[: wrong.numel() // 100] += 0.5  # 1% of the elements far off
+    assert not outputs_agree(wrong.to(torch.bfloat16), base)
+    nan = base.float().clone()
+    nan.view(-1)[3] = float("nan")
+    assert not outputs_agree(nan.to(torch.bfloat16), base)
+
+
+def test_a_stage_keeps_the_current_choice_unless_a_candidate_is_clearly_faster():
+    shape = SearchShape(*WORKLOADS["c5"])
+    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
+    base = search.incumbent()
+    candidates = [_with_attention(base, launch) for launch in ATTENTION_LAUNCHES]
+    current = next(c for c in candidates if c.config_id == base.config_id)
+    x = torch.zeros(4, 1)
+    search.legal = lambda config, device: True
+
+    def timings(table):
+        search._time = lambda config, _x: table.get(config.config_id, 100.0)
+
+    # a 0.5% "win" is noise: the current choice stays
+    timings({current.config_id: 50.0, candidates[0].config_id: 49.75})
+    assert search._best(candidates, x, current).config == current
+    # a 5% win replaces it
+    timings({current.config_id: 50.0, candidates[0].config_id: 47.5})
+    assert search._best(candidates, x, current).config == candidates[0]
+    # when the current choice is not among the candidates the fastest wins
+    timings({candidates[1].config_id: 10.0})
+    assert search._best(candidates[:3], x, hip_config()).config == candidates[1]

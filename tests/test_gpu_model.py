@@ -220,3 +220,28 @@ def test_default_resolution_on_gfx950_selects_the_hip_program(gpu_device):
     with torch.inference_mode():
         model(x)
     assert model.describe_execution_path()["planned_config_id"] == hip_config().config_id
+
+
+def test_default_resolution_selects_the_published_registry_entry(gpu_device):
+    """A shape published in the deployment registry for this environment runs
+    the published program without configure_execution (the reference's
+    exact-match resolution, deployment/registry.py)."""
+
+    from deployment.environment import EnvironmentFingerprint, ImplementationScope
+    from deployment.registry import ShapeFingerprint, resolve_deployed_config
+
+    config = TransformerConfig(64, 256, 512, 8, 2048, 4, True)
+    published = resolve_deployed_config(
+        hardware=EnvironmentFingerprint.detect(gpu_device, scope=ImplementationScope.RESIDENT),
+        shape=ShapeFingerprint(
+            batch_size=64, qkv_dim=512, heads=8, seq_len=256, layers=4, causal=True, ffn_dim=2048,
+            dtype="bfloat16", padding_ratio=0.0, input_scale=1.0,
+        ),
+    )
+    if published is None:
+        pytest.skip("the registry holds no entry for this environment's fingerprint")
+    model = _model(config, xavier_init_weights(config, seed=3), gpu_device, torch.bfloat16)
+    x = generate_input(config, seed=3).to(torch.bfloat16).to(gpu_device)
+    with torch.inference_mode():
+        model(x)
+    assert model.describe_execution_path()["planned_config_id"] == published.config_id
