@@ -144,6 +144,44 @@ int sah_norm(
     int norm_kind, int block_rows, int num_warps,
     sah_stream_t stream);
 
+typedef enum {
+  SAH_ACTIVATION_NONE = 0,
+  SAH_ACTIVATION_GELU_EXACT = 1 /* 0.5 v (1 + erf(v / sqrt(2))) */
+} sah_activation;
+
+/*
+ * Linear layer with a fused epilogue:
+ *   y = round_to(dtype, act(x weight^T + bias))
+ * fp32 accumulation; the bias (optional, NULL for none) is added in fp32 and
+ * the activation evaluated in fp32 before the single rounding.
+ *
+ * Replaces the reference's
+ *   _linear_exact_gelu_kernel + prevalidated_triton_linear_exact_gelu
+ *     (solution/kernels/ffn/triton_linear_exact_gelu.py:69-137, 182-234)   activation = GELU_EXACT
+ *   the FFN input projection + exact GELU of the TORCH path
+ *     (solution/transformer.py:828-842)
+ * x: [rows, in_features] with row stride x_row_stride; weight: [out_features,
+ * in_features] contiguous (nn.Linear layout); bias: [out_features]; y: [rows,
+ * out_features] with row stride y_row_stride.  x, weight, bias and y share
+ * dtype (SAH_DTYPE_BF16 or SAH_DTYPE_F16).  in_features must be a multiple of
+ * 64 and out_features of 256; strides multiples of 8 elements; x, weight and y
+ * 16-byte aligned, bias 8-byte aligned.  Launch: (block_m, block_n, block_k,
+ * num_warps, num_stages) = (256, 256, 64, 8, 2), see
+ * sah_linear_launch_supported().
+ */
+int sah_linear(
+    const void* x, const void* weight, const void* bias, void* y,
+    int64_t rows, int64_t in_features, int64_t out_features,
+    int64_t x_row_stride, int64_t y_row_stride,
+    int dtype, int activation,
+    int block_m, int block_n, int block_k, int num_warps, int num_stages,
+    sah_stream_t stream);
+
+/* 1 if sah_linear implements this launch, else 0 (mirrors the reference's
+ * _launch_config_is_valid, solution/kernels/ffn/triton_linear_exact_gelu.py:29-45). */
+int sah_linear_launch_supported(int block_m, int block_n, int block_k, int num_warps,
+                                int num_stages);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,295 @@
+// Linear layer with a fused bias + exact-GELU epilogue, for gfx950 (CDNA4).
+//
+// Same contract as the reference's fused FFN input projection
+// (solution/kernels/ffn/triton_linear_exact_gelu.py:69-137):
+//   y = GELU(x W^T + b),  GELU(v) = 0.5 v (1 + erf(v / sqrt(2)))
+// with fp32 accumulation, the bias added in fp32, the activation evaluated in
+// fp32 and one rounding to the output dtype.  With the activation switched off
+// the same kernel is a plain Linear (bias optional).
+//
+// MI355X formulation:
+//  * 256 x 256 output tile per workgroup of 8 wavefronts (2 x 4), each wave
+//    owning 128 rows x 64 columns; K advances 64 at a time through a
+//    double-buffered LDS stage (rows padded by 16 bytes, conflict-free 16-byte
+//    operand reads) with one barrier per K step.
+//  * The product is computed transposed, Y^T = W X^T, with
+//    v_mfma_f32_32x32x16_{bf16,f16}: both operands are 16-byte row chunks of
+//    the row-major x and W tiles, and every lane's accumulator column is one
+//    output row holding runs of 4 consecutive output columns, so the epilogue
+//    packs them into 8-byte LDS writes and the tile leaves through LDS as
+//    fully coalesced 16-byte stores.
+//  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
+//    over the 8 XCDs) works on a contiguous run of tiles: the x rows of a
+//    run's tiles are shared in that XCD's L2.
+
+#include <cmath>
+
+#include "sah_common.hpp"
+
+namespace sah {
+namespace {
+
+constexpr int kBM = 256;              // output rows per workgroup
+constexpr int kBN = 256;              // output columns per workgroup
+constexpr int kBK = 64;               // K per stage
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRow = kBK + 8;         // LDS operand row (elements), 16-byte pad
+constexpr int kOutRow = kBN + 8;      // LDS output staging row (elements)
+
+struct LinearParams {
+  const void* x;     // [rows][K], row stride x_ld
+  const void* w;     // [N][K], contiguous
+  const void* bias;  // [N] or null, same dtype as x
+  void* y;           // [rows][N], row stride y_ld
+  int64_t rows, x_ld, y_ld;
+  int n, k;
+  int tiles_n, num_tiles;
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// GELU(v) = v * Phi(v) with Phi(v) = erfc(-v / sqrt(2)) / 2, and erfc(x) for
+// x >= 0 from Abramowitz & Stegun 7.1.26:
+//   erfc(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-x^2),
+//   t = 1 / (1 + p x),  |erf error| <= 1.5e-7,
+// so Phi(v) = 1 - erfc(|v|/sqrt 2) / 2 for v >= 0 and erfc(|v|/sqrt 2) / 2 for
+// v < 0.  Using erfc directly on the negative side avoids the cancellation of
+// 1 + erf(v / sqrt 2): against float64 exact GELU, the bf16 results of this
+// form differ (by one ulp) on fewer elements than fp32 1 + erff(...) does
+// (199 vs 404 of 200 000 N(0, 1.4) inputs, measured on the CPU), at about
+// half the VALU work of a general-purpose erff (one reciprocal, one exp2).
+__device__ __forceinline__ float gelu_exact(float v) {
+  const float x = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(x * (x * -1.4426950408889634f));
+  const float half_erfc = 0.5f * (poly * t) * e;
+  const float phi = v >= 0.0f ? 1.0f - half_erfc : half_erfc;
+  return v * phi;
+}
+
+template <typename T, bool GELU>
+__global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
+  typedef typename Vec8<T>::type V8;
+  typedef typename Vec8<T>::half_type V4;
+
+  // Two operand stages of x and W rows; after the K loop the same bytes hold
+  // the output tile.
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * 2 * kBM * kRow * sizeof(T)];
+  T(*x_lds)[kBM][kRow] = reinterpret_cast<T(*)[kBM][kRow]>(smem);
+  T(*w_lds)[kBN][kRow] = reinterpret_cast<T(*)[kBN][kRow]>(smem + 2 * kBM * kRow * sizeof(T));
+  T(*y_lds)[kOutRow] = reinterpret_cast<T(*)[kOutRow]>(smem);
+  static_assert(kBM * kOutRow * sizeof(T) <= sizeof(smem), "output staging must fit");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  const int wave_m = wave >> 2;  // 128-row slab
+  const int wave_n = wave & 3;   // 64-column slab
+
+  // ---- workgroup id -> tile, contiguous runs per XCD.
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7;
+  const int local = bid >> 3;
+  const int per = p.num_tiles >> 3;
+  const int rem = p.num_tiles & 7;
+  const int logical =
+      xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int tile_m = logical / p.tiles_n;
+  const int tile_n = logical - tile_m * p.tiles_n;
+  const int64_t m0 = (int64_t)tile_m * kBM;
+  const int n0 = tile_n * kBN;
+
+  const T* xg = static_cast<const T*>(p.x);
+  const T* wg = static_cast<const T*>(p.w);
+
+  // ---- staging: 4 chunks of 16 bytes of x and of W per thread and K step.
+  // Chunk c = tid + kThreads * i is row c / 8, elements 8 (c % 8) .. + 7.
+  u32x4 x_pref[4], w_pref[4];
+  auto load_step = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c >> 3;
+      const int kc = (c & 7) * 8;
+      const int64_t m = m0 + row;
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (m < p.rows) raw = load16(xg + m * p.x_ld + k0 + kc);
+      x_pref[i] = raw;
+      w_pref[i] = load16(wg + (int64_t)(n0 + row) * p.k + k0 + kc);
+    }
+  };
+  auto store_step = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c >> 3;
+      const int kc = (c & 7) * 8;
+      *reinterpret_cast<u32x4*>(&x_lds[stage][row][kc]) = x_pref[i];
+      *reinterpret_cast<u32x4*>(&w_lds[stage][row][kc]) = w_pref[i];
+    }
+  };
+
+  // acc[i][j]: Y^T block of 32 columns (i) x 32 rows (j); lane = one row.
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int steps = p.k / kBK;
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+
+  for (int s = 0; s < steps; ++s) {
+    const int stage = s & 1;
+    const bool has_next = s + 1 < steps;
+    if (has_next) load_step((s + 1) * kBK);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      V8 wf[2], xf[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        wf[i] = *reinterpret_cast<const V8*>(&w_lds[stage][wave_n * 64 + 32 * i + l32][16 * kk + 8 * half]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xf[j] = *reinterpret_cast<const V8*>(&x_lds[stage][wave_m * 128 + 32 * j + l32][16 * kk + 8 * half]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(wf[i], xf[j], acc[i][j]);
+    }
+    if (has_next) store_step(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: bias, activation, one rounding; stage the tile in LDS.
+  // Accumulator register r of acc[i][j] holds output column
+  // 32 i + 8 (r / 4) + 4 half + r % 4 (within the wave's slab) of row 32 j + l32.
+  const T* bg = static_cast<const T*>(p.bias);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n_l = wave_n * 64 + 32 * i + 8 * g + 4 * half;
+      float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (bg != nullptr) {
+        const V4 raw = *reinterpret_cast<const V4*>(bg + n0 + n_l);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bv[q] = to_f32(raw[q]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        V4 out;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v = acc[i][j][4 * g + q] + bv[q];
+          if (GELU) v = gelu_exact(v);
+          out[q] = from_f32<T>(v);
+        }
+        *reinterpret_cast<V4*>(&y_lds[wave_m * 128 + 32 * j + l32][n_l]) = out;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- coalesced 16-byte stores of the valid rows.
+  T* yg = static_cast<T*>(p.y);
+#pragma unroll
+  for (int s2 = 0; s2 < (kBM * kBN / 8) / kThreads; ++s2) {
+    const int c = tid + kThreads * s2;
+    const int row = c >> 5;          // 32 chunks of 8 elements per row
+    const int col = (c & 31) * 8;
+    const int64_t m = m0 + row;
+    if (m < p.rows) store16(yg + m * p.y_ld + n0 + col, *reinterpret_cast<const u32x4*>(&y_lds[row][col]));
+  }
+}
+
+template <typename T, bool GELU>
+int launch_linear(const LinearParams& prm, hipStream_t stream) {
+  hipLaunchKernelGGL((linear_kernel<T, GELU>), dim3(prm.num_tiles), dim3(kThreads), 0, stream, prm);
+  return check_hip(hipGetLastError(), "linear kernel launch");
+}
+
+}  // namespace
+}  // namespace sah
+
+using namespace sah;
+
+extern "C" int sah_linear_launch_supported(int block_m, int block_n, int block_k, int num_warps,
+                                           int num_stages) {
+  return block_m == kBM && block_n == kBN && block_k == kBK && num_warps == kWaves && num_stages == 2;
+}
+
+extern "C" int sah_linear(const void* x, const void* weight, const void* bias, void* y,
+                          int64_t rows, int64_t in_features, int64_t out_features,
+                          int64_t x_row_stride, int64_t y_row_stride, int dtype, int activation,
+                          int block_m, int block_n, int block_k, int num_warps, int num_stages,
+                          sah_stream_t stream) {
+  if (!sah_linear_launch_supported(block_m, block_n, block_k, num_warps, num_stages))
+    return fail(SAH_ERR_UNSUPPORTED,
+                "sah_linear: launch (%d, %d, %d, %d, %d) is not implemented (256, 256, 64, 8, 2)",
+                block_m, block_n, block_k, num_warps, num_stages);
+  if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16)
+    return fail(SAH_ERR_UNSUPPORTED, "sah_linear: dtype %d is not bf16 or f16", dtype);
+  if (activation != SAH_ACTIVATION_NONE && activation != SAH_ACTIVATION_GELU_EXACT)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_linear: unknown activation %d", activation);
+  if (rows < 0 || in_features <= 0 || out_features <= 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_linear: bad sizes rows=%lld in=%lld out=%lld",
+                (long long)rows, (long long)in_features, (long long)out_features);
+  if (in_features % kBK != 0 || out_features % kBN != 0 || in_features > (1 << 20) ||
+      out_features > (1 << 20))
+    return fail(SAH_ERR_UNSUPPORTED,
+                "sah_linear: in_features must be a multiple of %d and out_features of %d "
+                "(got %lld, %lld)",
+                kBK, kBN, (long long)in_features, (long long)out_features);
+  if (x_row_stride < in_features || y_row_stride < out_features || x_row_stride % 8 != 0 ||
+      y_row_stride % 8 != 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_linear: row strides must cover the row and be multiples of 8 elements "
+                "(x %lld, y %lld)",
+                (long long)x_row_stride, (long long)y_row_stride);
+  if (rows == 0) return SAH_OK;
+  if (x == nullptr || weight == nullptr || y == nullptr)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_linear: null tensor pointer");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(y) ||
+      (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 7u) != 0))
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_linear: x, weight and y must be 16-byte aligned, bias 8-byte aligned");
+  const int64_t tiles_m = (rows + kBM - 1) / kBM;
+  const int64_t tiles_n = out_features / kBN;
+  if (tiles_m * tiles_n > INT32_MAX)
+    return fail(SAH_ERR_UNSUPPORTED, "sah_linear: %lld rows is too many", (long long)rows);
+
+  LinearParams prm;
+  prm.x = x;
+  prm.w = weight;
+  prm.bias = bias;
+  prm.y = y;
+  prm.rows = rows;
+  prm.x_ld = x_row_stride;
+  prm.y_ld = y_row_stride;
+  prm.n = (int)out_features;
+  prm.k = (int)in_features;
+  prm.tiles_n = (int)tiles_n;
+  prm.num_tiles = (int)(tiles_m * tiles_n);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool gelu = activation == SAH_ACTIVATION_GELU_EXACT;
+  if (dtype == SAH_DTYPE_BF16)
+    return gelu ? launch_linear<bf16, true>(prm, s) : launch_linear<bf16, false>(prm, s);
+  return gelu ? launch_linear<f16, true>(prm, s) : launch_linear<f16, false>(prm, s);
+}

@@ -93,6 +93,7 @@ class FFNBackend(_StrEnum):
     TRITON_EXACT_GELU = "triton_exact_gelu"
     TRITON_LINEAR_EXACT_GELU = "triton_linear_exact_gelu"
     TRITON_FUSED_MLP_BOUNDARY = "triton_fused_mlp_boundary"
+    HIP_LINEAR_EXACT_GELU = "hip_linear_exact_gelu"
 
 
 class ResidualNormBackend(_StrEnum):
@@ -555,10 +556,13 @@ class ConfigSpec:
         triton_ffn = program.ffn is FFNBackend.TRITON_EXACT_GELU
         if triton_ffn != (schedule.ffn_launch is not None):
             raise ValueError("ffn_launch must be present exactly for Triton Exact-GELU")
-        fused_ffn_input = program.ffn is FFNBackend.TRITON_LINEAR_EXACT_GELU
+        fused_ffn_input = program.ffn in {
+            FFNBackend.TRITON_LINEAR_EXACT_GELU,
+            FFNBackend.HIP_LINEAR_EXACT_GELU,
+        }
         if fused_ffn_input != (schedule.ffn_input_launch is not None):
             raise ValueError(
-                "ffn_input_launch must be present exactly for Triton Linear Exact-GELU"
+                "ffn_input_launch must be present exactly for Triton or HIP Linear Exact-GELU"
             )
 
     @property
@@ -646,17 +650,24 @@ HIP_LONG_SEQUENCE_ATTENTION_LAUNCH = AttentionLaunchParams(
 HIP_DEFAULT_NORM_LAUNCH = NormLaunchParams(block_rows=4, num_warps=4)
 
 
+# The launch of the HIP Linear + exact-GELU kernel (csrc/linear_gelu.hip).
+HIP_LINEAR_LAUNCH = GemmLaunchParams(block_m=256, block_n=256, block_k=64, num_warps=8, num_stages=2)
+
+
 def hip_config(
     *,
     microbatch_size: int | None = None,
     graph: bool = False,
     attention_launch: AttentionLaunchParams = HIP_DEFAULT_ATTENTION_LAUNCH,
     norm_launch: NormLaunchParams = HIP_DEFAULT_NORM_LAUNCH,
+    fused_ffn_input: bool = False,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
     norms and HIP initial norm, projections and FFN in the model dtype on
     hipBLASLt.  ``microbatch_size`` selects the streamed schedule, ``graph``
-    the graph-replay runtime (one HIP graph per input signature)."""
+    the graph-replay runtime (one HIP graph per input signature),
+    ``fused_ffn_input`` the HIP Linear + bias + exact-GELU FFN input
+    projection instead of hipBLASLt followed by GELU."""
 
     if graph and microbatch_size is not None:
         raise ValueError("the graph runtime and the streamed schedule are exclusive")
@@ -674,7 +685,7 @@ def hip_config(
             precision_plan=PrecisionPlan.INPUT_DTYPE,
             qkv_materialization=QKVMaterialization.VIEW,
             attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
-            ffn=FFNBackend.TORCH,
+            ffn=FFNBackend.HIP_LINEAR_EXACT_GELU if fused_ffn_input else FFNBackend.TORCH,
             residual_norm=ResidualNormBackend.HIP_FUSED,
             initial_norm=InitialNormBackend.HIP,
         ),
@@ -683,6 +694,7 @@ def hip_config(
             attention_launch=attention_launch,
             residual_norm_launch=norm_launch,
             initial_norm_launch=norm_launch,
+            ffn_input_launch=HIP_LINEAR_LAUNCH if fused_ffn_input else None,
             microbatch_size=microbatch_size,
         ),
     )
@@ -696,6 +708,7 @@ __all__ = [
     "HIP_ATTENTION_BACKENDS",
     "HIP_DEFAULT_ATTENTION_LAUNCH",
     "HIP_DEFAULT_NORM_LAUNCH",
+    "HIP_LINEAR_LAUNCH",
     "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",
     "HIP_RESIDUAL_NORM_BACKENDS",
     "LAUNCHED_ATTENTION_BACKENDS",

@@ -1,0 +1,19 @@
+"""gfx950 FFN primitives."""
+
+from .hip_linear_gelu import (
+    HIP_LINEAR_BACKEND,
+    HIP_LINEAR_EXACT_GELU_BACKEND,
+    can_use_hip_linear_exact_gelu,
+    hip_linear_exact_gelu_available,
+    prevalidated_hip_linear,
+    prevalidated_hip_linear_exact_gelu,
+)
+
+__all__ = [
+    "HIP_LINEAR_BACKEND",
+    "HIP_LINEAR_EXACT_GELU_BACKEND",
+    "can_use_hip_linear_exact_gelu",
+    "hip_linear_exact_gelu_available",
+    "prevalidated_hip_linear",
+    "prevalidated_hip_linear_exact_gelu",
+]

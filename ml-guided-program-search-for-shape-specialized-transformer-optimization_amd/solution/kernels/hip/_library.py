@@ -25,6 +25,8 @@ SAH_ERR_UNSUPPORTED = 2
 SAH_ERR_HIP = 3
 SAH_ERR_WORKSPACE = 4
 
+SAH_ACTIVATION_NONE = 0
+SAH_ACTIVATION_GELU_EXACT = 1
 SAH_NORM_LAYER = 0
 SAH_NORM_RMS = 1
 
@@ -63,6 +65,8 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
         [_ptr] * 4 + [_i64, _i64, ctypes.c_float] + [_int] * 6 + [_ptr],
         _int,
     ),
+    "sah_linear": ([_ptr] * 4 + [_i64] * 5 + [_int] * 2 + [_int] * 5 + [_ptr], _int),
+    "sah_linear_launch_supported": ([_int] * 5, _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -158,6 +162,8 @@ __all__ = [
     "EXPORTED_SYMBOLS",
     "HipLibraryError",
     "LIBRARY_PATH",
+    "SAH_ACTIVATION_GELU_EXACT",
+    "SAH_ACTIVATION_NONE",
     "SAH_NORM_LAYER",
     "SAH_NORM_RMS",
     "check_status",

@@ -139,6 +139,7 @@ class HardwareCapabilities:
     hip_streaming_dh64_attention: bool | None = None
     hip_residual_norm: bool = False
     hip_initial_norm: bool = False
+    hip_linear_exact_gelu: bool = False
 
     @property
     def is_gfx950(self) -> bool:
@@ -185,6 +186,7 @@ class HardwareCapabilities:
             hip_streaming_dh64_attention=hip_available,
             hip_residual_norm=hip_available,
             hip_initial_norm=hip_available,
+            hip_linear_exact_gelu=hip_available,
         )
 
 
@@ -425,6 +427,45 @@ class PlanBuilder:
     ) -> None:
         backend = config.program.ffn
         if backend is FFNBackend.TORCH:
+            return
+        if backend is FFNBackend.HIP_LINEAR_EXACT_GELU:
+            # The fused input projection of the reference's
+            # TRITON_LINEAR_EXACT_GELU branch (solution/plan_builder.py:825-866),
+            # for 16-bit models with native-dtype weights.
+            from .kernels.ffn.hip_linear_gelu import launch_config_is_valid, supported_features
+
+            field = "program.ffn"
+            _validate_hip_common(context, hardware, hardware.hip_linear_exact_gelu, field, reject)
+            if context.dtype not in {torch.float16, torch.bfloat16}:
+                reject("unsupported_dtype", field, "HIP Linear + Exact-GELU runs on FP16 and BF16 models")
+            if config.program.ffn_input_projection is not ProjectionBackend.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    "program.ffn_input_projection",
+                    "HIP Linear + Exact-GELU multiplies the native-dtype input weights",
+                )
+            if config.program.precision_plan is not PrecisionPlan.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    "program.precision_plan",
+                    "HIP Linear + Exact-GELU writes the activation in the model dtype",
+                )
+            if context.ffn_dim is None or not supported_features(context.d_model, context.ffn_dim):
+                reject(
+                    "unsupported_shape",
+                    field,
+                    "HIP Linear + Exact-GELU needs d_model % 64 == 0 and ffn_dim % 256 == 0",
+                )
+            launch = config.schedule.ffn_input_launch
+            assert launch is not None
+            if not launch_config_is_valid(
+                launch.block_m, launch.block_n, launch.block_k, launch.num_warps, launch.num_stages
+            ):
+                reject(
+                    "unsupported_launch_value",
+                    "schedule.ffn_input_launch",
+                    "HIP Linear + Exact-GELU implements (256, 256, 64, 8, 2)",
+                )
             return
         what = "torch.compile FFN" if backend is FFNBackend.COMPILED else f"Triton FFN {backend.value}"
         _unavailable(reject, "program.ffn", what)

@@ -42,6 +42,7 @@ from .config import (
     AttentionOutputBridge,
     AttentionOutputLayout,
     ConfigSpec,
+    FFNBackend,
     InitialNormBackend,
     PrecisionPlan,
     ProjectionBackend,
@@ -417,13 +418,41 @@ class _TransformerBlock(nn.Module):
         plan: ExecutionPlan,
         observation: _ExecutionObservation | None,
     ) -> torch.Tensor:
-        """Exact-GELU FFN (reference :816-1062, TORCH branch)."""
+        """Exact-GELU FFN (reference :816-1062): the TORCH branch, or the fused
+        Linear + bias + exact GELU input projection (reference :898-935, here
+        the gfx950 kernel) followed by the output projection."""
 
-        projected = self.ffn_in.forward_backend(normalized, plan.ffn_input_projection_backend)
-        input_compute_dtype = _dtype_name(projected.dtype)
-        if plan.ffn_activation_output_dtype == "float32":
-            projected = projected.float()
-        hidden = F.gelu(projected, approximate="none")
+        if plan.ffn_backend is FFNBackend.HIP_LINEAR_EXACT_GELU:
+            from .kernels.ffn.hip_linear_gelu import (
+                HIP_LINEAR_EXACT_GELU_BACKEND,
+                prevalidated_hip_linear_exact_gelu,
+            )
+
+            launch = plan.ffn_input_launch
+            if launch is None:
+                raise RuntimeError("HIP Linear + Exact-GELU plan is missing launch parameters")
+            hidden, marker = prevalidated_hip_linear_exact_gelu(
+                normalized,
+                self.ffn_in.weight,
+                self.ffn_in.bias,
+                block_m=launch.block_m,
+                block_n=launch.block_n,
+                block_k=launch.block_k,
+                num_warps=launch.num_warps,
+                num_stages=launch.num_stages,
+            )
+            _strict_backend_marker(
+                marker,
+                expected_marker=HIP_LINEAR_EXACT_GELU_BACKEND,
+                planned_backend=plan.ffn_backend.value,
+            )
+            input_compute_dtype = _dtype_name(hidden.dtype)
+        else:
+            projected = self.ffn_in.forward_backend(normalized, plan.ffn_input_projection_backend)
+            input_compute_dtype = _dtype_name(projected.dtype)
+            if plan.ffn_activation_output_dtype == "float32":
+                projected = projected.float()
+            hidden = F.gelu(projected, approximate="none")
         update = self.ffn_out.forward_backend(hidden, plan.ffn_output_projection_backend)
         if observation is not None:
             observation.ffn_input_projection_backends.append(plan.ffn_input_projection_backend.value)

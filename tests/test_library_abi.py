@@ -97,3 +97,37 @@ def test_custom_op_has_a_fake_implementation():
     q = torch.empty(2, 16, 1000, 64, device="meta", dtype=torch.bfloat16)
     out = torch.ops.shape_aware_hip.streaming_dh64_causal_attention_bsd(q, q, q, 0.125, 128, 64, 4, 2)
     assert out.shape == (2, 1000, 1024) and out.device.type == "meta"
+
+
+def test_linear_entry_validates_before_launch():
+    """sah_linear's launch table and argument checks (no kernel runs)."""
+
+    from solution.kernels.ffn.hip_linear_gelu import launch_config_is_valid
+
+    library = _library.load_library()
+    assert library.sah_linear_launch_supported(256, 256, 64, 8, 2) == 1
+    for launch in [(128, 128, 64, 8, 2), (256, 256, 32, 8, 2), (256, 256, 64, 4, 2), (256, 256, 64, 8, 3)]:
+        assert library.sah_linear_launch_supported(*launch) == 0
+        assert not launch_config_is_valid(*launch)
+    assert launch_config_is_valid(256, 256, 64, 8, 2)
+    assert not launch_config_is_valid(True, 256, 64, 8, 2)
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    args = dict(rows=4, k=1024, n=4096, ldx=1024, ldy=4096, dtype=2, act=1)
+
+    def call(**over):
+        a = {**args, **over}
+        launch = over.get("launch", (256, 256, 64, 8, 2))
+        return library.sah_linear(fake, fake, None, fake, a["rows"], a["k"], a["n"], a["ldx"], a["ldy"],
+                                  a["dtype"], a["act"], *launch, None)
+
+    assert call(launch=(128, 128, 64, 8, 2)) == _library.SAH_ERR_UNSUPPORTED
+    assert call(k=1000) == _library.SAH_ERR_UNSUPPORTED and b"multiple" in library.sah_last_error()
+    assert call(n=1000) == _library.SAH_ERR_UNSUPPORTED
+    assert call(dtype=0) == _library.SAH_ERR_UNSUPPORTED
+    assert call(act=5) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ldx=1020) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(rows=-1) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(rows=0) == _library.SAH_OK  # nothing to do, nothing launched
+    misaligned = ctypes.c_void_p(4096 + 8)
+    status = library.sah_linear(misaligned, fake, None, fake, 4, 1024, 4096, 1024, 4096, 2, 1, 256, 256, 64, 8, 2, None)
+    assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()

@@ -54,6 +54,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         hip_streaming_dh64_attention=True,
         hip_residual_norm=True,
         hip_initial_norm=True,
+        hip_linear_exact_gelu=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -327,3 +328,42 @@ def test_streamed_executor_writes_chunks_into_the_preallocated_output():
                               forward_chunk=lambda chunk, mask, destination: chunk - 1,
                               write_into_output=True)
     assert torch.equal(copied, value - 1)
+
+
+def test_fused_ffn_input_plans_and_rejections():
+    """The HIP Linear + exact-GELU FFN backend: accepted for 16-bit inference on
+    gfx950 with its launch, rejected with structured reasons otherwise (the
+    reference's TRITON_LINEAR_EXACT_GELU rules, solution/plan_builder.py:825-866)."""
+
+    import dataclasses
+
+    from solution.config import FFNBackend, GemmLaunchParams, PrecisionPlan
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    fused = hip_config(fused_ffn_input=True)
+    assert fused.program.ffn is FFNBackend.HIP_LINEAR_EXACT_GELU
+    assert fused.schedule.ffn_input_launch == GemmLaunchParams(256, 256, 64, 8, 2)
+    assert ConfigSpec.from_dict(fused.to_dict()) == fused
+    plan = builder.build(fused, _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4), _gfx950())
+    assert plan.ffn_backend is FFNBackend.HIP_LINEAR_EXACT_GELU
+    assert plan.expected_trace.to_dict()["ffn_activation_output_dtype"] == "bfloat16"
+    streamed = builder.build(hip_streamed_config(fused_ffn_input=True), _context(), _gfx950())
+    assert streamed.use_streamed_execution and streamed.ffn_input_launch is not None
+    # the launch is part of the schedule exactly when the fused backend is selected
+    with pytest.raises(ValueError, match="ffn_input_launch"):
+        dataclasses.replace(fused, schedule=dataclasses.replace(fused.schedule, ffn_input_launch=None))
+    unavailable = builder.evaluate(fused, _context(), _gfx950(hip_linear_exact_gelu=False))
+    assert ("program.ffn", "backend_unavailable") in codes(unavailable)
+    odd_ffn = builder.evaluate(fused, _context(ffn=4000), _gfx950())
+    assert ("program.ffn", "unsupported_shape") in codes(odd_ffn)
+    wrong_launch = dataclasses.replace(
+        fused, schedule=dataclasses.replace(fused.schedule, ffn_input_launch=GemmLaunchParams(128, 128, 32, 4, 2))
+    )
+    assert ("schedule.ffn_input_launch", "unsupported_launch_value") in codes(builder.evaluate(wrong_launch, _context(), _gfx950()))
+    # an fp32-GELU precision plan needs FP16 projections, which the fused
+    # backend does not multiply: the program itself is invalid
+    with pytest.raises(ValueError, match="FP16 backend"):
+        dataclasses.replace(fused.program, precision_plan=PrecisionPlan.FP16_FFN_INPUT_FP32_GELU)
+    training = builder.evaluate(fused, _context(grad=True), _gfx950())
+    assert ("program.ffn", "requires_inference") in codes(training)
