@@ -13,16 +13,24 @@ build:
   streamed long-sequence scope; eager or graph replay for resident shapes);
 * every candidate is first checked by PlanBuilder (an illegal candidate is
   never timed);
-* it is a coordinate search: attention launch, then norm launch, then runtime,
-  each stage keeping the best of the previous ones; a stage replaces the
+* it is a coordinate search: attention launch, then norm launch, then the FFN
+  input projection (hipBLASLt + GELU, or the fused HIP Linear + exact-GELU
+  kernel where the plan builder accepts it), then runtime, each stage keeping
+  the best of the previous ones; a stage replaces the
   current choice only when a candidate is faster by more than ``min_gain``
   (1% by default), because repeated timings of one program differ by a few
   tenths of a percent and a noise-level "win" is not a reason to deploy a
   different program;
-* the winner must agree with the default program's output on the same input
-  (finite; at most 0.1% of elements outside |err| <= 2e-2 or <= 1e-2 |ref|;
-  max-abs at most 0.125, i.e. within the bf16 residual-stream noise) before
-  it is published with ``deployment.registry.publish_deployed_config``.
+* before it is published with ``deployment.registry.publish_deployed_config``
+  a winner that differs from the default program must be no less accurate
+  than the default program on the same input, both measured against the same
+  model run in fp32 on the portable (torch) path: finite, max-abs error within
+  1.25x of the default program's (or within 2e-2), mean-abs error within 1.25x
+  (+1e-4), and at most 1.25x as many elements outside |err| <= 2e-2 or
+  |err| <= 1e-2 |ref| (+1e-4 of the elements).  Two bf16 programs with
+  different rounding orders differ by more than an elementwise gate between
+  them allows (one ulp of a residual-stream value of magnitude 4-8 is 0.03),
+  so the gate compares each with fp32 instead.
 
 Long sequences are timed on a slice of ``timed_sequences`` sequences (the
 streamed chunks are identical, so the per-sequence cost carries over); the
@@ -48,8 +56,10 @@ from pathlib import Path
 import torch
 
 from solution.config import (
+    HIP_LINEAR_LAUNCH,
     AttentionLaunchParams,
     ConfigSpec,
+    FFNBackend,
     NormLaunchParams,
     RuntimeBackend,
     hip_config,
@@ -119,6 +129,23 @@ def _with_attention(config: ConfigSpec, launch: AttentionLaunchParams) -> Config
     return dataclasses.replace(config, schedule=dataclasses.replace(config.schedule, attention_launch=launch))
 
 
+def _ffn_variants(config: ConfigSpec) -> list[ConfigSpec]:
+    """The FFN input projection choices: hipBLASLt followed by GELU, or the
+    fused HIP Linear + bias + exact-GELU kernel with its launch."""
+
+    torch_ffn = dataclasses.replace(
+        config,
+        program=dataclasses.replace(config.program, ffn=FFNBackend.TORCH),
+        schedule=dataclasses.replace(config.schedule, ffn_input_launch=None),
+    )
+    fused = dataclasses.replace(
+        config,
+        program=dataclasses.replace(config.program, ffn=FFNBackend.HIP_LINEAR_EXACT_GELU),
+        schedule=dataclasses.replace(config.schedule, ffn_input_launch=HIP_LINEAR_LAUNCH),
+    )
+    return [torch_ffn, fused]
+
+
 def _with_norms(config: ConfigSpec, launch: NormLaunchParams) -> ConfigSpec:
     schedule = dataclasses.replace(
         config.schedule, residual_norm_launch=launch, initial_norm_launch=launch
@@ -126,15 +153,25 @@ def _with_norms(config: ConfigSpec, launch: NormLaunchParams) -> ConfigSpec:
     return dataclasses.replace(config, schedule=schedule)
 
 
-def outputs_agree(candidate: torch.Tensor, incumbent: torch.Tensor) -> bool:
-    """The publication gate between two bf16 programs of the same model."""
+def _errors(output: torch.Tensor, reference: torch.Tensor) -> tuple[float, float, int]:
+    err = (output.float() - reference.float()).abs()
+    outside = ~((err <= 2e-2) | (err <= 1e-2 * reference.float().abs()))
+    return float(err.max()), float(err.mean()), int(outside.sum())
+
+
+def no_less_accurate(candidate: torch.Tensor, incumbent: torch.Tensor, reference: torch.Tensor) -> bool:
+    """The publication gate: ``candidate`` is no less accurate than
+    ``incumbent`` against the fp32 ``reference`` of the same model and input."""
 
     if not bool(torch.isfinite(candidate).all()):
         return False
-    got, want = candidate.float(), incumbent.float()
-    err = (got - want).abs()
-    outside = ~((err <= 2e-2) | (err <= 1e-2 * want.abs()))
-    return bool(outside.float().mean() <= 1e-3) and float(err.max()) <= 0.125
+    c_max, c_mean, c_out = _errors(candidate, reference)
+    i_max, i_mean, i_out = _errors(incumbent, reference)
+    return (
+        c_max <= max(1.25 * i_max, 2e-2)
+        and c_mean <= 1.25 * i_mean + 1e-4
+        and c_out <= 1.25 * i_out + 1e-4 * reference.numel()
+    )
 
 
 class HipLaunchSearch:
@@ -242,6 +279,7 @@ class HipLaunchSearch:
         base = incumbent
         base = self._best([_with_attention(base, launch) for launch in ATTENTION_LAUNCHES], timed, base).config
         base = self._best([_with_norms(base, launch) for launch in NORM_LAUNCHES], timed, base).config
+        base = self._best(_ffn_variants(base), timed, base).config
         winner = self._best(
             _runtime_variants(base, streamed=self.streamed, batch=math.gcd(self.shape.batch_size, self.timed)),
             timed,
@@ -249,16 +287,35 @@ class HipLaunchSearch:
         )
         return winner, Measurement(incumbent, incumbent_ms)
 
-    def agrees_with_incumbent(self, winner: ConfigSpec, x: torch.Tensor) -> bool:
-        """Compares on the timed rows: every runtime variant divides them."""
+    def _fp32_reference(self, sample: torch.Tensor) -> torch.Tensor:
+        """The same weights in fp32 on the portable (torch) path."""
 
+        from solution.config import portable_config, portable_streamed_config
+        from solution.transformer import UserOptimizedTransformer
+
+        reference = UserOptimizedTransformer(self.model.config)
+        reference.load_state_dict(self.model.state_dict())
+        reference = reference.to(device=sample.device, dtype=torch.float32).eval()
+        reference.configure_execution(
+            config=portable_streamed_config() if self.streamed else portable_config()
+        )
+        with torch.inference_mode():
+            return reference(sample.float())
+
+    def agrees_with_incumbent(self, winner: ConfigSpec, x: torch.Tensor) -> bool:
+        """Compares on the timed rows (every runtime variant divides them)."""
+
+        incumbent = self.incumbent()
+        if winner.config_id == incumbent.config_id:
+            return True
         sample = x[: self.timed].contiguous()
         with torch.inference_mode():
-            self.model.configure_execution(config=self.incumbent())
+            self.model.configure_execution(config=incumbent)
             want = self.model(sample)
             self.model.configure_execution(config=winner)
             got = self.model(sample)
-        return outputs_agree(got, want)
+        reference = self._fp32_reference(sample)
+        return no_less_accurate(got, want, reference)
 
 
 def _seeded_model(shape: SearchShape, device: torch.device, seed: int) -> torch.nn.Module:

@@ -14,18 +14,19 @@ from autotune.hip_launch_search import (
     WORKLOADS,
     HipLaunchSearch,
     SearchShape,
+    _ffn_variants,
     _runtime_variants,
     _with_attention,
     _with_norms,
-    outputs_agree,
+    no_less_accurate,
 )
 from solution.config import RuntimeBackend, hip_config
 from solution.plan_builder import HardwareCapabilities
 from solution.shape14.defaults import hip_streamed_config
 
 
-def _gfx950() -> HardwareCapabilities:
-    return HardwareCapabilities(
+def _gfx950(**overrides) -> HardwareCapabilities:
+    values = dict(
         device_type="cuda", compute_capability=(9, 5), shared_memory_per_block=65536,
         mem_efficient_sdp=False, cudnn_sdp=False, cudnn_available=False, torch_compile=False,
         triton_shape13_attention=False, triton_dh8_attention=False, triton_residual_norm=False,
@@ -33,6 +34,8 @@ def _gfx950() -> HardwareCapabilities:
         triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
         hip_residual_norm=True, hip_initial_norm=True,
     )
+    values.update(overrides)
+    return HardwareCapabilities(**values)
 
 
 def test_space_is_every_kernel_launch():
@@ -81,17 +84,21 @@ def test_resident_space_offers_eager_and_graph_replay():
 
 def test_publication_gate():
     generator = torch.Generator().manual_seed(0)
-    base = (torch.randn(2, 64, 128, generator=generator) * 3).to(torch.bfloat16)
-    assert outputs_agree(base, base)
-    noisy = base.float().clone()
-    noisy.view(-1)[:10] += 0.0625  # one bf16 ulp at |x| in [8, 16) on a few elements
-    assert outputs_agree(noisy.to(torch.bfloat16), base)
-    wrong = base.float().clone()
+    exact = torch.randn(2, 64, 128, generator=generator) * 3
+    # two 16-bit programs: each carries its own accumulated rounding noise
+    incumbent = (exact + 0.01 * torch.randn(exact.shape, generator=generator)).to(torch.bfloat16)
+    other = (exact + 0.01 * torch.randn(exact.shape, generator=generator)).to(torch.bfloat16)
+    assert no_less_accurate(incumbent, incumbent, exact)
+    assert no_less_accurate(other, incumbent, exact)
+    wrong = other.float().clone()
     wrong.view(-1)[: wrong.numel() // 100] += 0.5  # 1% of the elements far off
-    assert not outputs_agree(wrong.to(torch.bfloat16), base)
-    nan = base.float().clone()
+    assert not no_less_accurate(wrong.to(torch.bfloat16), incumbent, exact)
+    nan = other.float().clone()
     nan.view(-1)[3] = float("nan")
-    assert not outputs_agree(nan.to(torch.bfloat16), base)
+    assert not no_less_accurate(nan.to(torch.bfloat16), incumbent, exact)
+    # a dropped term: every element off by a little more than the noise
+    biased = (exact + 0.05).to(torch.bfloat16)
+    assert not no_less_accurate(biased, incumbent, exact)
 
 
 def test_a_stage_keeps_the_current_choice_unless_a_candidate_is_clearly_faster():
@@ -115,3 +122,19 @@ def test_a_stage_keeps_the_current_choice_unless_a_candidate_is_clearly_faster()
     # when the current choice is not among the candidates the fastest wins
     timings({candidates[1].config_id: 10.0})
     assert search._best(candidates[:3], x, hip_config()).config == candidates[1]
+
+
+def test_ffn_stage_offers_hipblaslt_and_the_fused_kernel():
+    from solution.config import FFNBackend
+
+    shape = SearchShape(*WORKLOADS["c5"])
+    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_linear_exact_gelu=True))
+    base = search.incumbent()
+    variants = _ffn_variants(base)
+    assert [v.program.ffn for v in variants] == [FFNBackend.TORCH, FFNBackend.HIP_LINEAR_EXACT_GELU]
+    assert variants[0] == base  # the default program is one of them
+    device = torch.device("cuda")
+    assert all(search.legal(v, device) for v in variants)
+    # without the kernel the fused variant is rejected, never timed
+    no_kernel = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_linear_exact_gelu=False))
+    assert not no_kernel.legal(variants[1], device)
