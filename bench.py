@@ -25,11 +25,13 @@ profiles/attn_fwd_c5_chunk_traffic.md as ``key = value`` lines and is
 reported only while ``source_digest`` there equals the digest of the current
 attention source and default launch (otherwise null).
 
-``--kernel attention|norm|copy`` runs one kernel alone at the workload's
-per-chunk shape (for rocprofv3 runs) and prints each launch's duration:
-attention over a packed [2, S, 3D] QKV view exactly as the model hands it
-over, the fused residual+LayerNorm at one chunk's block boundary, or a
-1 GiB device copy used to calibrate the memory counters.  Attention runs with
+``--kernel attention|norm|copy|linear|linear-torch`` runs one kernel alone at
+the workload's per-chunk shape (for rocprofv3 runs) and prints each launch's
+duration: attention over a packed [2, S, 3D] QKV view exactly as the model
+hands it over, the fused residual+LayerNorm at one chunk's block boundary, a
+1 GiB device copy used to calibrate the memory counters, the fused HIP
+Linear + bias + exact GELU of the FFN input projection ([2S, D] -> [2S, F]),
+or the same projection as hipBLASLt F.linear followed by torch's exact GELU.  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 """
 
@@ -314,6 +316,19 @@ def kernel_alone(kind: str, repeat: int) -> int:
             target = torch.empty_like(source)
             run = lambda: target.copy_(source)
             work = "1 GiB read + 1 GiB written per launch"
+        elif kind in ("linear", "linear-torch"):
+            from solution.kernels.ffn import prevalidated_hip_linear_exact_gelu
+
+            rows, ffn = batch * seq, w["ffn_dim"]
+            x = torch.randn(rows, width, generator=generator, device=device, dtype=torch.bfloat16)
+            bound = math.sqrt(6.0 / (width + ffn))
+            weight = ((torch.rand(ffn, width, generator=generator, device=device) * 2 - 1) * bound).to(torch.bfloat16)
+            bias = torch.zeros(ffn, device=device, dtype=torch.bfloat16)
+            if kind == "linear":
+                run = lambda: prevalidated_hip_linear_exact_gelu(x, weight, bias)
+            else:
+                run = lambda: torch.nn.functional.gelu(torch.nn.functional.linear(x, weight, bias), approximate="none")
+            work = f"{2 * rows * width * ffn / 1e12:.3f} TFLOP per launch"
         else:
             raise SystemExit(f"unknown kernel {kind!r}")
         torch.cuda.synchronize()
@@ -383,7 +398,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--kernel", choices=("attention", "norm", "copy"),
+    parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()
