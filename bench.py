@@ -25,13 +25,14 @@ profiles/attn_fwd_c5_chunk_traffic.md as ``key = value`` lines and is
 reported only while ``source_digest`` there equals the digest of the current
 attention source and default launch (otherwise null).
 
-``--kernel attention|norm|copy|linear|linear-torch`` runs one kernel alone at
+``--kernel attention|norm|copy|linear|linear-torch|gelu|gelu-torch`` runs one kernel alone at
 the workload's per-chunk shape (for rocprofv3 runs) and prints each launch's
 duration: attention over a packed [2, S, 3D] QKV view exactly as the model
 hands it over, the fused residual+LayerNorm at one chunk's block boundary, a
 1 GiB device copy used to calibrate the memory counters, the fused HIP
 Linear + bias + exact GELU of the FFN input projection ([2S, D] -> [2S, F]),
-or the same projection as hipBLASLt F.linear followed by torch's exact GELU.  Attention runs with
+the same projection as hipBLASLt F.linear followed by torch's exact GELU, or
+the exact GELU alone on the [2S, F] hidden tensor (HIP in place, or torch).  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 """
 
@@ -329,6 +330,16 @@ def kernel_alone(kind: str, repeat: int) -> int:
             else:
                 run = lambda: torch.nn.functional.gelu(torch.nn.functional.linear(x, weight, bias), approximate="none")
             work = f"{2 * rows * width * ffn / 1e12:.3f} TFLOP per launch"
+        elif kind in ("gelu", "gelu-torch"):
+            from solution.kernels.ffn import prevalidated_hip_exact_gelu
+
+            hidden = torch.randn(batch * seq, w["ffn_dim"], generator=generator, device=device,
+                                 dtype=torch.bfloat16)
+            if kind == "gelu":
+                run = lambda: prevalidated_hip_exact_gelu(hidden, out=hidden)
+            else:
+                run = lambda: torch.nn.functional.gelu(hidden, approximate="none")
+            work = f"{2 * 2 * hidden.numel() / 1e9:.3f} GB per launch"
         else:
             raise SystemExit(f"unknown kernel {kind!r}")
         torch.cuda.synchronize()
@@ -398,7 +409,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch"),
+    parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()

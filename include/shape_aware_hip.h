@@ -182,6 +182,24 @@ int sah_linear(
 int sah_linear_launch_supported(int block_m, int block_n, int block_k, int num_warps,
                                 int num_stages);
 
+/*
+ * Exact GELU of a contiguous 16-bit tensor: y = round_to(dtype, GELU(x)),
+ * GELU(v) = 0.5 v (1 + erf(v / sqrt(2))) evaluated in fp32.  y may be x.
+ *
+ * Replaces the reference's
+ *   _exact_gelu_kernel + prevalidated_triton_exact_gelu
+ *     (solution/kernels/ffn/triton_exact_gelu.py:50-118)
+ *   F.gelu(approximate="none") of the TORCH FFN path (solution/transformer.py:828-831)
+ * x, y: n elements of dtype SAH_DTYPE_BF16 or SAH_DTYPE_F16, 16-byte aligned.
+ * block_size elements per workgroup of num_warps wavefronts; block_size must be
+ * 512 x num_warps x {1, 2, 4, 8}, num_warps in {1, 2, 4, 8}.
+ */
+int sah_gelu(const void* x, void* y, int64_t n, int dtype, int block_size, int num_warps,
+             sah_stream_t stream);
+
+/* 1 if sah_gelu implements (block_size, num_warps), else 0. */
+int sah_gelu_launch_supported(int block_size, int num_warps);
+
 #ifdef __cplusplus
 }
 #endif

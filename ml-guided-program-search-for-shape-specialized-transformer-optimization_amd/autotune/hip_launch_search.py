@@ -14,9 +14,9 @@ build:
 * every candidate is first checked by PlanBuilder (an illegal candidate is
   never timed);
 * it is a coordinate search: attention launch, then norm launch, then the FFN
-  input projection (hipBLASLt + GELU, or the fused HIP Linear + exact-GELU
-  kernel where the plan builder accepts it), then runtime, each stage keeping
-  the best of the previous ones; a stage replaces the
+  activation path (hipBLASLt + torch GELU, hipBLASLt + the HIP elementwise
+  GELU, or the fused HIP Linear + exact-GELU kernel where the plan builder
+  accepts it), then runtime, each stage keeping the best of the previous ones; a stage replaces the
   current choice only when a candidate is faster by more than ``min_gain``
   (1% by default), because repeated timings of one program differ by a few
   tenths of a percent and a noise-level "win" is not a reason to deploy a
@@ -56,6 +56,7 @@ from pathlib import Path
 import torch
 
 from solution.config import (
+    HIP_GELU_LAUNCH,
     HIP_LINEAR_LAUNCH,
     AttentionLaunchParams,
     ConfigSpec,
@@ -130,20 +131,24 @@ def _with_attention(config: ConfigSpec, launch: AttentionLaunchParams) -> Config
 
 
 def _ffn_variants(config: ConfigSpec) -> list[ConfigSpec]:
-    """The FFN input projection choices: hipBLASLt followed by GELU, or the
-    fused HIP Linear + bias + exact-GELU kernel with its launch."""
+    """The FFN activation paths: hipBLASLt followed by torch's GELU or by the
+    HIP elementwise GELU, or the fused HIP Linear + bias + exact-GELU kernel,
+    each with its launch."""
 
-    torch_ffn = dataclasses.replace(
-        config,
-        program=dataclasses.replace(config.program, ffn=FFNBackend.TORCH),
-        schedule=dataclasses.replace(config.schedule, ffn_input_launch=None),
-    )
-    fused = dataclasses.replace(
-        config,
-        program=dataclasses.replace(config.program, ffn=FFNBackend.HIP_LINEAR_EXACT_GELU),
-        schedule=dataclasses.replace(config.schedule, ffn_input_launch=HIP_LINEAR_LAUNCH),
-    )
-    return [torch_ffn, fused]
+    def with_ffn(backend: FFNBackend, ffn_launch=None, ffn_input_launch=None) -> ConfigSpec:
+        return dataclasses.replace(
+            config,
+            program=dataclasses.replace(config.program, ffn=backend),
+            schedule=dataclasses.replace(
+                config.schedule, ffn_launch=ffn_launch, ffn_input_launch=ffn_input_launch
+            ),
+        )
+
+    return [
+        with_ffn(FFNBackend.TORCH),
+        with_ffn(FFNBackend.HIP_EXACT_GELU, ffn_launch=HIP_GELU_LAUNCH),
+        with_ffn(FFNBackend.HIP_LINEAR_EXACT_GELU, ffn_input_launch=HIP_LINEAR_LAUNCH),
+    ]
 
 
 def _with_norms(config: ConfigSpec, launch: NormLaunchParams) -> ConfigSpec:

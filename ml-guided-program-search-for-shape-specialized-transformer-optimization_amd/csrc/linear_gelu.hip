@@ -54,29 +54,6 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// GELU(v) = v * Phi(v) with Phi(v) = erfc(-v / sqrt(2)) / 2, and erfc(x) for
-// x >= 0 from Abramowitz & Stegun 7.1.26:
-//   erfc(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-x^2),
-//   t = 1 / (1 + p x),  |erf error| <= 1.5e-7,
-// so Phi(v) = 1 - erfc(|v|/sqrt 2) / 2 for v >= 0 and erfc(|v|/sqrt 2) / 2 for
-// v < 0.  Using erfc directly on the negative side avoids the cancellation of
-// 1 + erf(v / sqrt 2): against float64 exact GELU, the bf16 results of this
-// form differ (by one ulp) on fewer elements than fp32 1 + erff(...) does
-// (199 vs 404 of 200 000 N(0, 1.4) inputs, measured on the CPU), at about
-// half the VALU work of a general-purpose erff (one reciprocal, one exp2).
-__device__ __forceinline__ float gelu_exact(float v) {
-  const float x = fabsf(v) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  const float e = __builtin_amdgcn_exp2f(x * (x * -1.4426950408889634f));
-  const float half_erfc = 0.5f * (poly * t) * e;
-  const float phi = v >= 0.0f ? 1.0f - half_erfc : half_erfc;
-  return v * phi;
-}
-
 template <typename T, bool GELU>
 __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   typedef typename Vec8<T>::type V8;

@@ -94,6 +94,7 @@ class FFNBackend(_StrEnum):
     TRITON_LINEAR_EXACT_GELU = "triton_linear_exact_gelu"
     TRITON_FUSED_MLP_BOUNDARY = "triton_fused_mlp_boundary"
     HIP_LINEAR_EXACT_GELU = "hip_linear_exact_gelu"
+    HIP_EXACT_GELU = "hip_exact_gelu"
 
 
 class ResidualNormBackend(_StrEnum):
@@ -553,9 +554,9 @@ class ConfigSpec:
             raise ValueError(
                 "initial_norm_launch must be present exactly for Triton or HIP initial norm"
             )
-        triton_ffn = program.ffn is FFNBackend.TRITON_EXACT_GELU
-        if triton_ffn != (schedule.ffn_launch is not None):
-            raise ValueError("ffn_launch must be present exactly for Triton Exact-GELU")
+        elementwise_gelu = program.ffn in {FFNBackend.TRITON_EXACT_GELU, FFNBackend.HIP_EXACT_GELU}
+        if elementwise_gelu != (schedule.ffn_launch is not None):
+            raise ValueError("ffn_launch must be present exactly for Triton or HIP Exact-GELU")
         fused_ffn_input = program.ffn in {
             FFNBackend.TRITON_LINEAR_EXACT_GELU,
             FFNBackend.HIP_LINEAR_EXACT_GELU,
@@ -652,6 +653,10 @@ HIP_DEFAULT_NORM_LAUNCH = NormLaunchParams(block_rows=4, num_warps=4)
 
 # The launch of the HIP Linear + exact-GELU kernel (csrc/linear_gelu.hip).
 HIP_LINEAR_LAUNCH = GemmLaunchParams(block_m=256, block_n=256, block_k=64, num_warps=8, num_stages=2)
+# The default launch of the HIP elementwise exact GELU (csrc/gelu.hip): one
+# 16-byte chunk per thread, 8 wavefronts (6.1 TB/s on the C5 hidden tensor,
+# the fastest of the implemented launches on MI355X).
+HIP_GELU_LAUNCH = FFNLaunchParams(block_size=4096, num_warps=8)
 
 
 def hip_config(
@@ -660,14 +665,19 @@ def hip_config(
     graph: bool = False,
     attention_launch: AttentionLaunchParams = HIP_DEFAULT_ATTENTION_LAUNCH,
     norm_launch: NormLaunchParams = HIP_DEFAULT_NORM_LAUNCH,
-    fused_ffn_input: bool = False,
+    ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
-    norms and HIP initial norm, projections and FFN in the model dtype on
-    hipBLASLt.  ``microbatch_size`` selects the streamed schedule, ``graph``
-    the graph-replay runtime (one HIP graph per input signature),
-    ``fused_ffn_input`` the HIP Linear + bias + exact-GELU FFN input
-    projection instead of hipBLASLt followed by GELU."""
+    norms and HIP initial norm, projections in the model dtype on hipBLASLt,
+    the FFN activation by the HIP exact-GELU kernel.  ``microbatch_size`` selects the streamed schedule, ``graph``
+    the graph-replay runtime (one HIP graph per input signature).  ``ffn``
+    picks the FFN activation path: TORCH (hipBLASLt, then torch's exact GELU),
+    HIP_EXACT_GELU (hipBLASLt, then the HIP elementwise GELU) or
+    HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU)."""
+
+    ffn = FFNBackend(ffn)
+    if ffn not in {FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU}:
+        raise ValueError(f"FFN backend {ffn.value!r} is not part of the gfx950 program")
 
     if graph and microbatch_size is not None:
         raise ValueError("the graph runtime and the streamed schedule are exclusive")
@@ -685,7 +695,7 @@ def hip_config(
             precision_plan=PrecisionPlan.INPUT_DTYPE,
             qkv_materialization=QKVMaterialization.VIEW,
             attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
-            ffn=FFNBackend.HIP_LINEAR_EXACT_GELU if fused_ffn_input else FFNBackend.TORCH,
+            ffn=ffn,
             residual_norm=ResidualNormBackend.HIP_FUSED,
             initial_norm=InitialNormBackend.HIP,
         ),
@@ -694,7 +704,8 @@ def hip_config(
             attention_launch=attention_launch,
             residual_norm_launch=norm_launch,
             initial_norm_launch=norm_launch,
-            ffn_input_launch=HIP_LINEAR_LAUNCH if fused_ffn_input else None,
+            ffn_launch=HIP_GELU_LAUNCH if ffn is FFNBackend.HIP_EXACT_GELU else None,
+            ffn_input_launch=HIP_LINEAR_LAUNCH if ffn is FFNBackend.HIP_LINEAR_EXACT_GELU else None,
             microbatch_size=microbatch_size,
         ),
     )
@@ -708,6 +719,7 @@ __all__ = [
     "HIP_ATTENTION_BACKENDS",
     "HIP_DEFAULT_ATTENTION_LAUNCH",
     "HIP_DEFAULT_NORM_LAUNCH",
+    "HIP_GELU_LAUNCH",
     "HIP_LINEAR_LAUNCH",
     "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",
     "HIP_RESIDUAL_NORM_BACKENDS",

@@ -67,6 +67,8 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
     ),
     "sah_linear": ([_ptr] * 4 + [_i64] * 5 + [_int] * 2 + [_int] * 5 + [_ptr], _int),
     "sah_linear_launch_supported": ([_int] * 5, _int),
+    "sah_gelu": ([_ptr, _ptr, _i64, _int, _int, _int, _ptr], _int),
+    "sah_gelu_launch_supported": ([_int] * 2, _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -140,6 +140,7 @@ class HardwareCapabilities:
     hip_residual_norm: bool = False
     hip_initial_norm: bool = False
     hip_linear_exact_gelu: bool = False
+    hip_exact_gelu: bool = False
 
     @property
     def is_gfx950(self) -> bool:
@@ -187,6 +188,7 @@ class HardwareCapabilities:
             hip_residual_norm=hip_available,
             hip_initial_norm=hip_available,
             hip_linear_exact_gelu=hip_available,
+            hip_exact_gelu=hip_available,
         )
 
 
@@ -427,6 +429,36 @@ class PlanBuilder:
     ) -> None:
         backend = config.program.ffn
         if backend is FFNBackend.TORCH:
+            return
+        if backend is FFNBackend.HIP_EXACT_GELU:
+            # The elementwise activation of the reference's TRITON_EXACT_GELU
+            # branch (solution/plan_builder.py:870-900), for 16-bit models.
+            from .kernels.ffn.hip_exact_gelu import launch_config_is_valid as gelu_launch_is_valid
+
+            field = "program.ffn"
+            _validate_hip_common(context, hardware, hardware.hip_exact_gelu, field, reject)
+            if context.dtype not in {torch.float16, torch.bfloat16}:
+                reject("unsupported_dtype", field, "HIP Exact-GELU runs on FP16 and BF16 models")
+            if config.program.ffn_input_projection is not ProjectionBackend.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    "program.ffn_input_projection",
+                    "HIP Exact-GELU activates the model-dtype projection in place",
+                )
+            if config.program.precision_plan is not PrecisionPlan.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    "program.precision_plan",
+                    "HIP Exact-GELU writes the activation in the model dtype",
+                )
+            ffn_launch = config.schedule.ffn_launch
+            assert ffn_launch is not None
+            if not gelu_launch_is_valid(ffn_launch.block_size, ffn_launch.num_warps):
+                reject(
+                    "unsupported_launch_value",
+                    "schedule.ffn_launch",
+                    "HIP Exact-GELU needs block_size = 512 x num_warps x {1, 2, 4, 8}",
+                )
             return
         if backend is FFNBackend.HIP_LINEAR_EXACT_GELU:
             # The fused input projection of the reference's

@@ -59,14 +59,14 @@ def conservative_streamed_config() -> ConfigSpec:
 
 
 def hip_streamed_config(
-    *, microbatch_size: int = DEFAULT_MICROBATCH_SIZE, fused_ffn_input: bool = False
+    *, microbatch_size: int = DEFAULT_MICROBATCH_SIZE, ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU
 ) -> ConfigSpec:
     """The gfx950 long-sequence program with ordered microbatches."""
 
     return hip_config(
         microbatch_size=microbatch_size,
         attention_launch=HIP_LONG_SEQUENCE_ATTENTION_LAUNCH,
-        fused_ffn_input=fused_ffn_input,
+        ffn=ffn,
     )
 
 

@@ -418,9 +418,11 @@ class _TransformerBlock(nn.Module):
         plan: ExecutionPlan,
         observation: _ExecutionObservation | None,
     ) -> torch.Tensor:
-        """Exact-GELU FFN (reference :816-1062): the TORCH branch, or the fused
-        Linear + bias + exact GELU input projection (reference :898-935, here
-        the gfx950 kernel) followed by the output projection."""
+        """Exact-GELU FFN (reference :816-1062): the TORCH branch, the
+        elementwise Exact-GELU kernel after the input projection (reference
+        :945-965, here the gfx950 kernel), or the fused Linear + bias + exact
+        GELU input projection (reference :898-935, here the gfx950 kernel);
+        then the output projection."""
 
         if plan.ffn_backend is FFNBackend.HIP_LINEAR_EXACT_GELU:
             from .kernels.ffn.hip_linear_gelu import (
@@ -447,6 +449,21 @@ class _TransformerBlock(nn.Module):
                 planned_backend=plan.ffn_backend.value,
             )
             input_compute_dtype = _dtype_name(hidden.dtype)
+        elif plan.ffn_backend is FFNBackend.HIP_EXACT_GELU:
+            from .kernels.ffn.hip_exact_gelu import HIP_EXACT_GELU_BACKEND, prevalidated_hip_exact_gelu
+
+            launch = plan.ffn_launch
+            if launch is None:
+                raise RuntimeError("HIP Exact-GELU plan is missing launch parameters")
+            projected = self.ffn_in.forward_backend(normalized, plan.ffn_input_projection_backend)
+            input_compute_dtype = _dtype_name(projected.dtype)
+            # in place: the projection is a temporary of this block
+            hidden, marker = prevalidated_hip_exact_gelu(
+                projected, block_size=launch.block_size, num_warps=launch.num_warps, out=projected
+            )
+            _strict_backend_marker(
+                marker, expected_marker=HIP_EXACT_GELU_BACKEND, planned_backend=plan.ffn_backend.value
+            )
         else:
             projected = self.ffn_in.forward_backend(normalized, plan.ffn_input_projection_backend)
             input_compute_dtype = _dtype_name(projected.dtype)

@@ -32,7 +32,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         triton_shape13_attention=False, triton_dh8_attention=False, triton_residual_norm=False,
         triton_mixed_residual_norm=False, triton_initial_norm=False, triton_exact_gelu=False,
         triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
-        hip_residual_norm=True, hip_initial_norm=True,
+        hip_residual_norm=True, hip_initial_norm=True, hip_exact_gelu=True, hip_linear_exact_gelu=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -128,13 +128,18 @@ def test_ffn_stage_offers_hipblaslt_and_the_fused_kernel():
     from solution.config import FFNBackend
 
     shape = SearchShape(*WORKLOADS["c5"])
-    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_linear_exact_gelu=True))
+    search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
     base = search.incumbent()
     variants = _ffn_variants(base)
-    assert [v.program.ffn for v in variants] == [FFNBackend.TORCH, FFNBackend.HIP_LINEAR_EXACT_GELU]
-    assert variants[0] == base  # the default program is one of them
+    assert [v.program.ffn for v in variants] == [
+        FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU,
+    ]
+    assert variants[1] == base  # the default program is one of them
     device = torch.device("cuda")
     assert all(search.legal(v, device) for v in variants)
-    # without the kernel the fused variant is rejected, never timed
-    no_kernel = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_linear_exact_gelu=False))
-    assert not no_kernel.legal(variants[1], device)
+    # without the kernels the HIP variants are rejected, never timed
+    no_kernel = HipLaunchSearch(
+        torch.nn.Identity(), shape, hardware=_gfx950(hip_exact_gelu=False, hip_linear_exact_gelu=False)
+    )
+    assert no_kernel.legal(variants[0], device)
+    assert not no_kernel.legal(variants[1], device) and not no_kernel.legal(variants[2], device)

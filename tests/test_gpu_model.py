@@ -98,30 +98,32 @@ def test_hip_plan_matches_the_bf16_reference_path(gpu_device, shape):
         (2, 128, 2048, 32, 8192, 1),  # config 4 widths
     ],
 )
-def test_fused_ffn_input_plan_matches_the_bf16_reference_path(gpu_device, shape):
-    """The program with the HIP Linear + bias + exact-GELU FFN input
-    projection, end to end against the official bf16 path."""
+@pytest.mark.parametrize("ffn_backend", ["hip_linear_exact_gelu", "hip_exact_gelu"])
+def test_fused_ffn_input_plan_matches_the_bf16_reference_path(gpu_device, shape, ffn_backend):
+    """The programs with a HIP FFN activation path (the fused Linear + bias +
+    exact GELU, or hipBLASLt followed by the HIP elementwise GELU), end to end
+    against the official bf16 path."""
 
-    from solution.config import hip_config
+    from solution.config import FFNBackend, hip_config
 
     batch, seq, width, heads, ffn, layers = shape
-    print(f"fused ffn model parity {shape}", flush=True)
+    print(f"{ffn_backend} model parity {shape}", flush=True)
     config = TransformerConfig(batch, seq, width, heads, ffn, layers, True)
     state = xavier_init_weights(config, seed=4321)
     x = generate_input(config, seed=4321).to(torch.bfloat16)
     model = _model(config, state, gpu_device, torch.bfloat16)
-    model.configure_execution(config=hip_config(fused_ffn_input=True))
+    model.configure_execution(config=hip_config(ffn=FFNBackend(ffn_backend)))
     model.set_execution_observation(True)
     with torch.inference_mode():
         output = model(x.to(gpu_device))
     torch.cuda.synchronize()
     reference = forward(cast_state(state, torch.bfloat16), x, config)
     exact = forward(cast_state(cast_state(state, torch.bfloat16), torch.float32), x.float(), config)
-    _check_bf16_model(exact, reference.float(), output, f"fused ffn model {shape}")
+    _check_bf16_model(exact, reference.float(), output, f"{ffn_backend} model {shape}")
     description = model.describe_execution_path()
     observed = description["observed_execution_signature"]
     assert observed == description["expected_execution_signature"]
-    assert observed["ffn_backend"] == "hip_linear_exact_gelu"
+    assert observed["ffn_backend"] == ffn_backend
 
 
 def test_streamed_output_equals_its_chunks_bitwise(gpu_device):

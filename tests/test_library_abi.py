@@ -131,3 +131,21 @@ def test_linear_entry_validates_before_launch():
     misaligned = ctypes.c_void_p(4096 + 8)
     status = library.sah_linear(misaligned, fake, None, fake, 4, 1024, 4096, 1024, 4096, 2, 1, 256, 256, 64, 8, 2, None)
     assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()
+
+
+def test_gelu_entry_validates_before_launch():
+    from solution.kernels.ffn.hip_exact_gelu import launch_config_is_valid
+
+    library = _library.load_library()
+    for block_size in (256, 512, 1024, 2048, 4096, 8192, 16384, 3000):
+        for warps in (1, 2, 3, 4, 8):
+            assert launch_config_is_valid(block_size, warps) == bool(
+                library.sah_gelu_launch_supported(block_size, warps)
+            ), (block_size, warps)
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert library.sah_gelu(fake, fake, 10, 2, 256, 4, None) == _library.SAH_ERR_UNSUPPORTED
+    assert library.sah_gelu(fake, fake, 10, 0, 4096, 4, None) == _library.SAH_ERR_UNSUPPORTED
+    assert library.sah_gelu(fake, fake, -1, 2, 4096, 4, None) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert library.sah_gelu(fake, fake, 0, 2, 4096, 4, None) == _library.SAH_OK
+    status = library.sah_gelu(ctypes.c_void_p(4096 + 2), fake, 10, 2, 4096, 4, None)
+    assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()

@@ -55,6 +55,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         hip_residual_norm=True,
         hip_initial_norm=True,
         hip_linear_exact_gelu=True,
+        hip_exact_gelu=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -341,14 +342,14 @@ def test_fused_ffn_input_plans_and_rejections():
 
     builder = PlanBuilder()
     codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
-    fused = hip_config(fused_ffn_input=True)
+    fused = hip_config(ffn=FFNBackend.HIP_LINEAR_EXACT_GELU)
     assert fused.program.ffn is FFNBackend.HIP_LINEAR_EXACT_GELU
     assert fused.schedule.ffn_input_launch == GemmLaunchParams(256, 256, 64, 8, 2)
     assert ConfigSpec.from_dict(fused.to_dict()) == fused
     plan = builder.build(fused, _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4), _gfx950())
     assert plan.ffn_backend is FFNBackend.HIP_LINEAR_EXACT_GELU
     assert plan.expected_trace.to_dict()["ffn_activation_output_dtype"] == "bfloat16"
-    streamed = builder.build(hip_streamed_config(fused_ffn_input=True), _context(), _gfx950())
+    streamed = builder.build(hip_streamed_config(ffn=FFNBackend.HIP_LINEAR_EXACT_GELU), _context(), _gfx950())
     assert streamed.use_streamed_execution and streamed.ffn_input_launch is not None
     # the launch is part of the schedule exactly when the fused backend is selected
     with pytest.raises(ValueError, match="ffn_input_launch"):
@@ -367,3 +368,30 @@ def test_fused_ffn_input_plans_and_rejections():
         dataclasses.replace(fused.program, precision_plan=PrecisionPlan.FP16_FFN_INPUT_FP32_GELU)
     training = builder.evaluate(fused, _context(grad=True), _gfx950())
     assert ("program.ffn", "requires_inference") in codes(training)
+
+
+def test_elementwise_gelu_plans_and_rejections():
+    """The HIP elementwise exact GELU after the hipBLASLt input projection
+    (the reference's TRITON_EXACT_GELU rules, solution/plan_builder.py:870-900,
+    for 16-bit models)."""
+
+    import dataclasses
+
+    from solution.config import FFNBackend, FFNLaunchParams
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    gelu = hip_config(ffn=FFNBackend.HIP_EXACT_GELU)
+    assert gelu.schedule.ffn_launch == FFNLaunchParams(4096, 8) and gelu.schedule.ffn_input_launch is None
+    assert hip_config() == gelu  # the default gfx950 program
+    assert ConfigSpec.from_dict(gelu.to_dict()) == gelu
+    plan = builder.build(gelu, _context(), _gfx950())
+    assert plan.ffn_backend is FFNBackend.HIP_EXACT_GELU and plan.ffn_launch == FFNLaunchParams(4096, 8)
+    with pytest.raises(ValueError, match="ffn_launch"):
+        dataclasses.replace(gelu, schedule=dataclasses.replace(gelu.schedule, ffn_launch=None))
+    bad_launch = dataclasses.replace(gelu, schedule=dataclasses.replace(gelu.schedule, ffn_launch=FFNLaunchParams(256, 4)))
+    assert ("schedule.ffn_launch", "unsupported_launch_value") in codes(builder.evaluate(bad_launch, _context(), _gfx950()))
+    unavailable = builder.evaluate(gelu, _context(), _gfx950(hip_exact_gelu=False))
+    assert ("program.ffn", "backend_unavailable") in codes(unavailable)
+    with pytest.raises(ValueError, match="not part of the gfx950 program"):
+        hip_config(ffn=FFNBackend.TRITON_EXACT_GELU)
