@@ -25,14 +25,17 @@ profiles/attn_fwd_c5_chunk_traffic.md as ``key = value`` lines and is
 reported only while ``source_digest`` there equals the digest of the current
 attention source and default launch (otherwise null).
 
-``--kernel attention|norm|copy|linear|linear-torch|gelu|gelu-torch`` runs one kernel alone at
+``--kernel attention|norm|copy|linear|linear-torch|gelu|gelu-torch|qkv|qkv-torch`` runs one kernel alone at
 the workload's per-chunk shape (for rocprofv3 runs) and prints each launch's
 duration: attention over a packed [2, S, 3D] QKV view exactly as the model
 hands it over, the fused residual+LayerNorm at one chunk's block boundary, a
 1 GiB device copy used to calibrate the memory counters, the fused HIP
 Linear + bias + exact GELU of the FFN input projection ([2S, D] -> [2S, F]),
 the same projection as hipBLASLt F.linear followed by torch's exact GELU, or
-the exact GELU alone on the [2S, F] hidden tensor (HIP in place, or torch).  Attention runs with
+the exact GELU alone on the [2S, F] hidden tensor (HIP in place, or torch), or
+the packed QKV projection ([2S, D] -> 3 x [2, H, S, 64]): the HIP kernel with
+the head-major epilogue and seq-contiguous value, or hipBLASLt F.linear into
+the packed [2S, 3D] tensor the default program views.  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 """
 
@@ -330,6 +333,18 @@ def kernel_alone(kind: str, repeat: int) -> int:
             else:
                 run = lambda: torch.nn.functional.gelu(torch.nn.functional.linear(x, weight, bias), approximate="none")
             work = f"{2 * rows * width * ffn / 1e12:.3f} TFLOP per launch"
+        elif kind in ("qkv", "qkv-torch"):
+            from solution.kernels.projection import prevalidated_hip_qkv_native_bhsd
+
+            x = torch.randn(batch, seq, width, generator=generator, device=device, dtype=torch.bfloat16)
+            bound = math.sqrt(6.0 / (4 * width))
+            weight = ((torch.rand(3 * width, width, generator=generator, device=device) * 2 - 1) * bound).to(torch.bfloat16)
+            bias = torch.zeros(3 * width, device=device, dtype=torch.bfloat16)
+            if kind == "qkv":
+                run = lambda: prevalidated_hip_qkv_native_bhsd(x, weight, bias, num_heads=heads, value_layout="seq_major")
+            else:
+                run = lambda: torch.nn.functional.linear(x, weight, bias)
+            work = f"{2 * batch * seq * width * 3 * width / 1e12:.3f} TFLOP per launch"
         elif kind in ("gelu", "gelu-torch"):
             from solution.kernels.ffn import prevalidated_hip_exact_gelu
 
@@ -409,7 +424,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch"),
+    parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
+                                             "qkv", "qkv-torch"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()

@@ -200,6 +200,52 @@ int sah_gelu(const void* x, void* y, int64_t n, int dtype, int block_size, int n
 /* 1 if sah_gelu implements (block_size, num_warps), else 0. */
 int sah_gelu_launch_supported(int block_size, int num_warps);
 
+/* Value layouts sah_qkv_projection can write. */
+typedef enum {
+  SAH_QKV_VALUE_BHSD = 0,     /* [B, H, S, head_dim] contiguous, like query and key */
+  SAH_QKV_VALUE_SEQ_MAJOR = 1 /* [B, H, head_dim, value_seq_stride]: seq-contiguous
+                                 (the V^T operand sah_causal_attention_bsd reads directly) */
+} sah_qkv_value_layout;
+
+/*
+ * Packed QKV projection with a head-major epilogue:
+ *   qkv = round_to(dtype, x weight^T + bias)   (fp32 accumulation, bias in fp32)
+ * with output column c of [0, 3 d_model) written to
+ *   query (c < d_model), key (c < 2 d_model) or value, head (c % d_model) / head_dim,
+ *   element (c % d_model) % head_dim,
+ * and row r to token (r / seq_len, r % seq_len).  No [B, S, 3 d_model]
+ * intermediate exists.
+ *
+ * Replaces the reference's
+ *   _qkv_native_bhsd_kernel + prevalidated_triton_qkv_native_bhsd
+ *     (solution/kernels/projection/triton_qkv_layout.py:60-115, 170-230)
+ *   the packed QKV projection + split_qkv of the default path
+ *     (solution/transformer.py:432-435; solution/operators/projection/qkv_layout.py:22-50)
+ * x: [batch * seq_len, d_model] with row stride x_row_stride; weight:
+ * [3 d_model, d_model] contiguous (the packed qkv_proj weight, rows q | k | v);
+ * bias: [3 d_model] or NULL; query, key: [batch, heads, seq_len, head_dim]
+ * contiguous; value: the same, or (value_layout SAH_QKV_VALUE_SEQ_MAJOR)
+ * [batch, heads, head_dim, value_seq_stride] with tokens [seq_len,
+ * value_seq_stride) left untouched.  Shared dtype SAH_DTYPE_BF16 or
+ * SAH_DTYPE_F16.  d_model must be a multiple of 256 and head_dim = d_model /
+ * heads a multiple of 8; batch * seq_len below 2^31; x_row_stride and
+ * value_seq_stride multiples of 8; all tensors 16-byte aligned, bias 8-byte.
+ * Launch: (block_m, block_n, block_k, num_warps) = (256, 256, 64, 8), see
+ * sah_qkv_launch_supported().
+ */
+int sah_qkv_projection(
+    const void* x, const void* weight, const void* bias,
+    void* query, void* key, void* value,
+    int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads,
+    int64_t x_row_stride, int value_layout, int64_t value_seq_stride,
+    int dtype, int block_m, int block_n, int block_k, int num_warps,
+    sah_stream_t stream);
+
+/* 1 if sah_qkv_projection implements the launch, else 0 (mirrors the
+ * reference's _launch_config_is_valid,
+ * solution/kernels/projection/triton_qkv_layout.py:29-43). */
+int sah_qkv_launch_supported(int block_m, int block_n, int block_k, int num_warps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,15 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    over the 8 XCDs) works on a contiguous run of tiles: the x rows of a
 //    run's tiles are shared in that XCD's L2.
+//
+// The same GEMM with a head-major epilogue is the packed QKV projection of the
+// reference's native-layout path (solution/kernels/projection/
+// triton_qkv_layout.py:60-115): x [B*S, D] times the packed [3D, D] weight,
+// bias added in fp32, one rounding, and every output column scattered
+// straight into query / key / value as [B, H, S, head_dim] (no [B, S, 3D]
+// intermediate).  The value may instead be written seq-contiguous,
+// [B, H, head_dim, v_ld], the layout the attention kernel reads its V^T
+// operand from, which saves the attention's own transpose pass.
 
 #include <cmath>
 
@@ -37,14 +46,30 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kRow = kBK + 8;         // LDS operand row (elements), 16-byte pad
 constexpr int kOutRow = kBN + 8;      // LDS output staging row (elements)
 
+// Epilogues: row-major y (optionally through exact GELU), or the head-major
+// Q / K / V scatter.
+constexpr int kEpiRows = 0;
+constexpr int kEpiRowsGelu = 1;
+constexpr int kEpiHeads = 2;
+
 struct LinearParams {
   const void* x;     // [rows][K], row stride x_ld
   const void* w;     // [N][K], contiguous
   const void* bias;  // [N] or null, same dtype as x
-  void* y;           // [rows][N], row stride y_ld
+  void* y;           // [rows][N], row stride y_ld (row-major epilogues)
   int64_t rows, x_ld, y_ld;
   int n, k;
   int tiles_n, num_tiles;
+  // Head-major epilogue: output columns [0, D) -> q, [D, 2D) -> k,
+  // [2D, 3D) -> v, column c of a block -> head c / head_dim, element
+  // c % head_dim; row r -> token (r / seq_len, r % seq_len).
+  void* q;
+  void* kk;
+  void* v;
+  int64_t v_ld;      // seq stride of a seq-contiguous value
+  int seq_len, heads, head_dim, d_model;
+  int v_seq_major;   // value as [B][H][head_dim][v_ld] instead of [B][H][S][head_dim]
+  int seq_aligned;   // seq_len % 8 == 0: 8-token runs never cross a sequence
 };
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -54,10 +79,11 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <typename T, bool GELU>
+template <typename T, int EPI>
 __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
+  constexpr bool GELU = EPI == kEpiRowsGelu;
 
   // Two operand stages of x and W rows; after the K loop the same bytes hold
   // the output tile.
@@ -184,21 +210,82 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   }
   __syncthreads();
 
-  // ---- coalesced 16-byte stores of the valid rows.
-  T* yg = static_cast<T*>(p.y);
+  constexpr int kChunks = (kBM * kBN / 8) / kThreads;  // 16-byte chunks per thread
+  if constexpr (EPI != kEpiHeads) {
+    // ---- coalesced 16-byte stores of the valid rows.
+    T* yg = static_cast<T*>(p.y);
 #pragma unroll
-  for (int s2 = 0; s2 < (kBM * kBN / 8) / kThreads; ++s2) {
-    const int c = tid + kThreads * s2;
-    const int row = c >> 5;          // 32 chunks of 8 elements per row
-    const int col = (c & 31) * 8;
-    const int64_t m = m0 + row;
-    if (m < p.rows) store16(yg + m * p.y_ld + n0 + col, *reinterpret_cast<const u32x4*>(&y_lds[row][col]));
+    for (int s2 = 0; s2 < kChunks; ++s2) {
+      const int c = tid + kThreads * s2;
+      const int row = c >> 5;          // 32 chunks of 8 elements per row
+      const int col = (c & 31) * 8;
+      const int64_t m = m0 + row;
+      if (m < p.rows) store16(yg + m * p.y_ld + n0 + col, *reinterpret_cast<const u32x4*>(&y_lds[row][col]));
+    }
+  } else {
+    // ---- head-major scatter.  d_model is a multiple of kBN, so the whole
+    // tile belongs to one of q / k / v.  Token indices fit in 32 bits (the
+    // host checks rows < 2^31).
+    const int which = n0 / p.d_model;
+    const int c0 = n0 - which * p.d_model;
+    T* dst = static_cast<T*>(which == 0 ? p.q : which == 1 ? p.kk : p.v);
+    const unsigned seq = (unsigned)p.seq_len;
+    const int hd = p.head_dim;
+    if (which != 2 || !p.v_seq_major) {
+      // [B][H][S][hd]: a 16-byte chunk is 8 consecutive elements of one head
+      // (head_dim is a multiple of 8).
+#pragma unroll 4
+      for (int s2 = 0; s2 < kChunks; ++s2) {
+        const int c = tid + kThreads * s2;
+        const int row = c >> 5;
+        const int col = (c & 31) * 8;
+        const int64_t m = m0 + row;
+        if (m >= p.rows) continue;
+        const unsigned b = (unsigned)m / seq;
+        const unsigned s = (unsigned)m - b * seq;
+        const int within = c0 + col;
+        const int head = within / hd;
+        const int e = within - head * hd;
+        T* out = dst + (((int64_t)b * p.heads + head) * (int64_t)seq + s) * hd + e;
+        store16(out, *reinterpret_cast<const u32x4*>(&y_lds[row][col]));
+      }
+    } else {
+      // [B][H][hd][v_ld]: a 16-byte chunk is 8 consecutive tokens of one
+      // column, read down an LDS column (consecutive lanes take consecutive
+      // columns: conflict-free).
+#pragma unroll 4
+      for (int s2 = 0; s2 < kChunks; ++s2) {
+        const int c = tid + kThreads * s2;
+        const int col = c & (kBN - 1);
+        const int row0 = (c >> 8) * 8;
+        const int64_t m = m0 + row0;
+        if (m >= p.rows) continue;
+        const int within = c0 + col;
+        const int head = within / hd;
+        const int e = within - head * hd;
+        if (p.seq_aligned && m + 8 <= p.rows) {
+          const unsigned b = (unsigned)m / seq;
+          const unsigned s = (unsigned)m - b * seq;
+          V8 run;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) run[t] = y_lds[row0 + t][col];
+          T* out = dst + (((int64_t)b * p.heads + head) * hd + e) * p.v_ld + s;
+          store16(out, __builtin_bit_cast(u32x4, run));
+        } else {
+          for (int t = 0; t < 8 && m + t < p.rows; ++t) {
+            const unsigned b = (unsigned)(m + t) / seq;
+            const unsigned s = (unsigned)(m + t) - b * seq;
+            dst[(((int64_t)b * p.heads + head) * hd + e) * p.v_ld + s] = y_lds[row0 + t][col];
+          }
+        }
+      }
+    }
   }
 }
 
-template <typename T, bool GELU>
+template <typename T, int EPI>
 int launch_linear(const LinearParams& prm, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_kernel<T, GELU>), dim3(prm.num_tiles), dim3(kThreads), 0, stream, prm);
+  hipLaunchKernelGGL((linear_kernel<T, EPI>), dim3(prm.num_tiles), dim3(kThreads), 0, stream, prm);
   return check_hip(hipGetLastError(), "linear kernel launch");
 }
 
@@ -252,7 +339,7 @@ extern "C" int sah_linear(const void* x, const void* weight, const void* bias, v
   if (tiles_m * tiles_n > INT32_MAX)
     return fail(SAH_ERR_UNSUPPORTED, "sah_linear: %lld rows is too many", (long long)rows);
 
-  LinearParams prm;
+  LinearParams prm = {};
   prm.x = x;
   prm.w = weight;
   prm.bias = bias;
@@ -267,6 +354,81 @@ extern "C" int sah_linear(const void* x, const void* weight, const void* bias, v
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool gelu = activation == SAH_ACTIVATION_GELU_EXACT;
   if (dtype == SAH_DTYPE_BF16)
-    return gelu ? launch_linear<bf16, true>(prm, s) : launch_linear<bf16, false>(prm, s);
-  return gelu ? launch_linear<f16, true>(prm, s) : launch_linear<f16, false>(prm, s);
+    return gelu ? launch_linear<bf16, kEpiRowsGelu>(prm, s) : launch_linear<bf16, kEpiRows>(prm, s);
+  return gelu ? launch_linear<f16, kEpiRowsGelu>(prm, s) : launch_linear<f16, kEpiRows>(prm, s);
+}
+
+extern "C" int sah_qkv_launch_supported(int block_m, int block_n, int block_k, int num_warps) {
+  return block_m == kBM && block_n == kBN && block_k == kBK && num_warps == kWaves;
+}
+
+extern "C" int sah_qkv_projection(const void* x, const void* weight, const void* bias, void* query,
+                                  void* key, void* value, int64_t batch, int64_t seq_len,
+                                  int64_t d_model, int64_t heads, int64_t x_row_stride,
+                                  int value_layout, int64_t value_seq_stride, int dtype,
+                                  int block_m, int block_n, int block_k, int num_warps,
+                                  sah_stream_t stream) {
+  if (!sah_qkv_launch_supported(block_m, block_n, block_k, num_warps))
+    return fail(SAH_ERR_UNSUPPORTED,
+                "sah_qkv_projection: launch (%d, %d, %d, %d) is not implemented (256, 256, 64, 8)",
+                block_m, block_n, block_k, num_warps);
+  if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16)
+    return fail(SAH_ERR_UNSUPPORTED, "sah_qkv_projection: dtype %d is not bf16 or f16", dtype);
+  if (value_layout != SAH_QKV_VALUE_BHSD && value_layout != SAH_QKV_VALUE_SEQ_MAJOR)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_qkv_projection: unknown value layout %d", value_layout);
+  if (batch < 0 || seq_len <= 0 || d_model <= 0 || heads <= 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_qkv_projection: bad sizes batch=%lld seq_len=%lld d_model=%lld heads=%lld",
+                (long long)batch, (long long)seq_len, (long long)d_model, (long long)heads);
+  if (d_model % kBN != 0 || d_model > (1 << 18) || d_model % heads != 0 || (d_model / heads) % 8 != 0)
+    return fail(SAH_ERR_UNSUPPORTED,
+                "sah_qkv_projection: d_model must be a multiple of %d (at most 2^18) and split "
+                "into heads of a multiple of 8 elements (got d_model %lld, %lld heads)",
+                kBN, (long long)d_model, (long long)heads);
+  if (x_row_stride < d_model || x_row_stride % 8 != 0)
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_qkv_projection: x row stride %lld must cover d_model and be a multiple of 8",
+                (long long)x_row_stride);
+  if (value_layout == SAH_QKV_VALUE_SEQ_MAJOR && (value_seq_stride < seq_len || value_seq_stride % 8 != 0))
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_qkv_projection: value seq stride %lld must cover seq_len %lld and be a "
+                "multiple of 8",
+                (long long)value_seq_stride, (long long)seq_len);
+  if (batch == 0) return SAH_OK;
+  if (seq_len > INT32_MAX || batch > INT32_MAX / seq_len)
+    return fail(SAH_ERR_UNSUPPORTED, "sah_qkv_projection: batch x seq_len must be below 2^31");
+  if (x == nullptr || weight == nullptr || query == nullptr || key == nullptr || value == nullptr)
+    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_qkv_projection: null tensor pointer");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(query) || !aligned16(key) || !aligned16(value) ||
+      (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 7u) != 0))
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_qkv_projection: x, weight, query, key and value must be 16-byte aligned, "
+                "bias 8-byte aligned");
+  const int64_t rows = batch * seq_len;
+  const int64_t tiles_m = (rows + kBM - 1) / kBM;
+  const int64_t tiles_n = 3 * d_model / kBN;
+
+  LinearParams prm = {};
+  prm.x = x;
+  prm.w = weight;
+  prm.bias = bias;
+  prm.rows = rows;
+  prm.x_ld = x_row_stride;
+  prm.n = (int)(3 * d_model);
+  prm.k = (int)d_model;
+  prm.tiles_n = (int)tiles_n;
+  prm.num_tiles = (int)(tiles_m * tiles_n);
+  prm.q = query;
+  prm.kk = key;
+  prm.v = value;
+  prm.v_ld = value_layout == SAH_QKV_VALUE_SEQ_MAJOR ? value_seq_stride : 0;
+  prm.seq_len = (int)seq_len;
+  prm.heads = (int)heads;
+  prm.head_dim = (int)(d_model / heads);
+  prm.d_model = (int)d_model;
+  prm.v_seq_major = value_layout == SAH_QKV_VALUE_SEQ_MAJOR;
+  prm.seq_aligned = seq_len % 8 == 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return dtype == SAH_DTYPE_BF16 ? launch_linear<bf16, kEpiHeads>(prm, s)
+                                 : launch_linear<f16, kEpiHeads>(prm, s);
 }

@@ -79,6 +79,7 @@ class QKVMaterialization(_StrEnum):
     VIEW = "view"
     CONTIGUOUS = "contiguous"
     TRITON_NATIVE_BHSD = "triton_native_bhsd"
+    HIP_NATIVE_BHSD = "hip_native_bhsd"
 
 
 class AttentionOutputBridge(_StrEnum):
@@ -151,6 +152,10 @@ LAUNCHED_RESIDUAL_NORM_BACKENDS = frozenset(
 ) | HIP_RESIDUAL_NORM_BACKENDS
 LAUNCHED_INITIAL_NORM_BACKENDS = frozenset(
     {InitialNormBackend.TRITON_FP16, InitialNormBackend.HIP}
+)
+# QKV materializations produced by a projection kernel (they need qkv_launch).
+NATIVE_QKV_MATERIALIZATIONS = frozenset(
+    {QKVMaterialization.TRITON_NATIVE_BHSD, QKVMaterialization.HIP_NATIVE_BHSD}
 )
 
 _PROJECTION_FIELDS = (
@@ -532,9 +537,9 @@ class ConfigSpec:
             raise ValueError(
                 "attention_launch must be present exactly for Triton or HIP attention"
             )
-        native_qkv = program.qkv_materialization is QKVMaterialization.TRITON_NATIVE_BHSD
+        native_qkv = program.qkv_materialization in NATIVE_QKV_MATERIALIZATIONS
         if native_qkv != (schedule.qkv_launch is not None):
-            raise ValueError("qkv_launch must be present exactly for Triton native QKV")
+            raise ValueError("qkv_launch must be present exactly for Triton or HIP native QKV")
         fused_output_projection = (
             program.attention_output_bridge is AttentionOutputBridge.TRITON_BHSD_PROJECTION
             and program.residual_norm is not ResidualNormBackend.TRITON_LINEAR_MIXED
@@ -657,6 +662,9 @@ HIP_LINEAR_LAUNCH = GemmLaunchParams(block_m=256, block_n=256, block_k=64, num_w
 # 16-byte chunk per thread, 8 wavefronts (6.1 TB/s on the C5 hidden tensor,
 # the fastest of the implemented launches on MI355X).
 HIP_GELU_LAUNCH = FFNLaunchParams(block_size=4096, num_warps=8)
+# The launch of the HIP packed-QKV projection with the head-major epilogue
+# (csrc/linear_gelu.hip, sah_qkv_projection): the same GEMM core.
+HIP_QKV_LAUNCH = QKVLaunchParams(block_m=256, block_n=256, block_k=64, num_warps=8)
 
 
 def hip_config(
@@ -666,6 +674,7 @@ def hip_config(
     attention_launch: AttentionLaunchParams = HIP_DEFAULT_ATTENTION_LAUNCH,
     norm_launch: NormLaunchParams = HIP_DEFAULT_NORM_LAUNCH,
     ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU,
+    qkv: QKVMaterialization = QKVMaterialization.VIEW,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
     norms and HIP initial norm, projections in the model dtype on hipBLASLt,
@@ -673,11 +682,17 @@ def hip_config(
     the graph-replay runtime (one HIP graph per input signature).  ``ffn``
     picks the FFN activation path: TORCH (hipBLASLt, then torch's exact GELU),
     HIP_EXACT_GELU (hipBLASLt, then the HIP elementwise GELU) or
-    HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU)."""
+    HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU).  ``qkv``
+    picks how Q, K and V are produced: VIEW (hipBLASLt packed projection and
+    zero-copy views) or HIP_NATIVE_BHSD (the HIP projection writing
+    head-major Q / K and a seq-contiguous V straight from its epilogue)."""
 
     ffn = FFNBackend(ffn)
     if ffn not in {FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU}:
         raise ValueError(f"FFN backend {ffn.value!r} is not part of the gfx950 program")
+    qkv = QKVMaterialization(qkv)
+    if qkv not in {QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD}:
+        raise ValueError(f"QKV materialization {qkv.value!r} is not part of the gfx950 program")
 
     if graph and microbatch_size is not None:
         raise ValueError("the graph runtime and the streamed schedule are exclusive")
@@ -693,7 +708,7 @@ def hip_config(
             ffn_input_projection=ProjectionBackend.INPUT_DTYPE,
             ffn_output_projection=ProjectionBackend.INPUT_DTYPE,
             precision_plan=PrecisionPlan.INPUT_DTYPE,
-            qkv_materialization=QKVMaterialization.VIEW,
+            qkv_materialization=qkv,
             attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
             ffn=ffn,
             residual_norm=ResidualNormBackend.HIP_FUSED,
@@ -702,6 +717,7 @@ def hip_config(
         schedule=ScheduleConfig(
             runtime=runtime,
             attention_launch=attention_launch,
+            qkv_launch=HIP_QKV_LAUNCH if qkv is QKVMaterialization.HIP_NATIVE_BHSD else None,
             residual_norm_launch=norm_launch,
             initial_norm_launch=norm_launch,
             ffn_launch=HIP_GELU_LAUNCH if ffn is FFNBackend.HIP_EXACT_GELU else None,
@@ -721,9 +737,11 @@ __all__ = [
     "HIP_DEFAULT_NORM_LAUNCH",
     "HIP_GELU_LAUNCH",
     "HIP_LINEAR_LAUNCH",
+    "HIP_QKV_LAUNCH",
     "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",
     "HIP_RESIDUAL_NORM_BACKENDS",
     "LAUNCHED_ATTENTION_BACKENDS",
+    "NATIVE_QKV_MATERIALIZATIONS",
     "TRITON_ATTENTION_BACKENDS",
     "AttentionBackend",
     "AttentionLaunchParams",

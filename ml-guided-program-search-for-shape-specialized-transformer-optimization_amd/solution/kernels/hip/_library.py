@@ -27,6 +27,8 @@ SAH_ERR_WORKSPACE = 4
 
 SAH_ACTIVATION_NONE = 0
 SAH_ACTIVATION_GELU_EXACT = 1
+SAH_QKV_VALUE_BHSD = 0
+SAH_QKV_VALUE_SEQ_MAJOR = 1
 SAH_NORM_LAYER = 0
 SAH_NORM_RMS = 1
 
@@ -69,6 +71,11 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
     "sah_linear_launch_supported": ([_int] * 5, _int),
     "sah_gelu": ([_ptr, _ptr, _i64, _int, _int, _int, _ptr], _int),
     "sah_gelu_launch_supported": ([_int] * 2, _int),
+    "sah_qkv_projection": (
+        [_ptr] * 6 + [_i64] * 5 + [_int, _i64] + [_int] * 5 + [_ptr],
+        _int,
+    ),
+    "sah_qkv_launch_supported": ([_int] * 4, _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
@@ -166,6 +173,8 @@ __all__ = [
     "LIBRARY_PATH",
     "SAH_ACTIVATION_GELU_EXACT",
     "SAH_ACTIVATION_NONE",
+    "SAH_QKV_VALUE_BHSD",
+    "SAH_QKV_VALUE_SEQ_MAJOR",
     "SAH_NORM_LAYER",
     "SAH_NORM_RMS",
     "check_status",

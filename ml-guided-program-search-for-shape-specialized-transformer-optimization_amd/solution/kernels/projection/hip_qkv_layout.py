@@ -1,0 +1,260 @@
+"""Packed QKV projection straight into head-major Q / K / V on gfx950.
+
+Counterpart of the reference's native-layout QKV projection
+(solution/kernels/projection/triton_qkv_layout.py:1-300): the same
+``available / can_use / prevalidated / strict`` functions, the same
+``(query, key, value, marker)`` return value and the same strictness (an
+unsupported launch raises ValueError, ineligible inputs RuntimeError "...
+ineligible", a failed launch RuntimeError "... execution failed"; no
+fallback).  The reference kernel (:60-115) multiplies x [B*S, D] by the packed
+[3D, D] weight in fp32, adds the bias and stores the three D-column blocks as
+contiguous [B, H, S, D/H] tensors; this one does the same for bf16 or fp16
+operands with one rounding to the operand dtype (``sah_qkv_projection``,
+csrc/linear_gelu.hip).
+
+``value_layout="seq_major"`` writes the value block seq-contiguous instead,
+into a [B, H, D/H, S8] buffer (S8 = S rounded up to 8) returned as its
+[B, H, S, D/H] view with strides (H*dh*S8, dh*S8, 1, S8): the operand layout
+the gfx950 attention kernel reads V^T from, so the attention needs no
+transpose pass and no workspace.
+
+Differences in domain from the reference (fp16, D in {32, 128, 1024},
+S in {32, 128, 1024}, H in {1, 2, 4, 16}): bf16 or fp16, any batch and
+sequence length with B*S < 2^31, D a multiple of 256, head_dim a multiple of 8.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..hip._library import (
+    SAH_QKV_VALUE_BHSD,
+    SAH_QKV_VALUE_SEQ_MAJOR,
+    check_status,
+    dtype_code,
+    is_gfx950,
+    library_available,
+    load_library,
+    stream_handle,
+)
+
+HIP_QKV_NATIVE_BHSD_BACKEND = "hip_qkv_native_bhsd"
+DEFAULT_BLOCK_M = 256
+DEFAULT_BLOCK_N = 256
+DEFAULT_BLOCK_K = 64
+DEFAULT_NUM_WARPS = 8
+D_MODEL_MULTIPLE = 256
+VALUE_LAYOUTS = {"bhsd": SAH_QKV_VALUE_BHSD, "seq_major": SAH_QKV_VALUE_SEQ_MAJOR}
+_SUPPORTED_DTYPES = frozenset({torch.bfloat16, torch.float16})
+
+
+def launch_config_is_valid(block_m: int, block_n: int, block_k: int, num_warps: int) -> bool:
+    """The launch the gfx950 kernel implements (the C library's own table)."""
+
+    values = (block_m, block_n, block_k, num_warps)
+    if any(isinstance(value, bool) or not isinstance(value, int) for value in values):
+        return False
+    if library_available():
+        return bool(load_library().sah_qkv_launch_supported(*values))
+    return values == (DEFAULT_BLOCK_M, DEFAULT_BLOCK_N, DEFAULT_BLOCK_K, DEFAULT_NUM_WARPS)
+
+
+def _validate_launch_config(block_m: int, block_n: int, block_k: int, num_warps: int) -> None:
+    if not launch_config_is_valid(block_m, block_n, block_k, num_warps):
+        raise ValueError("unsupported HIP QKV native-layout launch configuration")
+
+
+def supported_shape(d_model: int, num_heads: int) -> bool:
+    """Model widths with a kernel instantiation."""
+
+    return (
+        d_model > 0
+        and num_heads > 0
+        and d_model % D_MODEL_MULTIPLE == 0
+        and d_model % num_heads == 0
+        and (d_model // num_heads) % 8 == 0
+    )
+
+
+def hip_qkv_native_bhsd_available() -> bool:
+    """Whether the gfx950 library loads in this process."""
+
+    return library_available()
+
+
+def can_use_hip_qkv_native_bhsd(
+    hidden_states: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    num_heads: int,
+    block_m: int = DEFAULT_BLOCK_M,
+    block_n: int = DEFAULT_BLOCK_N,
+    block_k: int = DEFAULT_BLOCK_K,
+    num_warps: int = DEFAULT_NUM_WARPS,
+) -> bool:
+    """The reference's eligibility rules (triton_qkv_layout.py:127-167) with
+    this kernel's dtypes and shapes; never raises."""
+
+    if not launch_config_is_valid(block_m, block_n, block_k, num_warps):
+        return False
+    tensors = [hidden_states, weight] + ([] if bias is None else [bias])
+    if not all(isinstance(item, torch.Tensor) for item in tensors):
+        return False
+    if isinstance(num_heads, bool) or not isinstance(num_heads, int):
+        return False
+    # No autograd: refused while grad is enabled.  Under no_grad /
+    # inference_mode the model's parameters (requires_grad=True) are plain
+    # operands; the reference passes detached fp16 shadows instead.
+    if torch.is_grad_enabled():
+        return False
+    if hidden_states.device.type != "cuda" or any(t.device != hidden_states.device for t in tensors):
+        return False
+    if hidden_states.ndim != 3 or hidden_states.dtype not in _SUPPORTED_DTYPES:
+        return False
+    batch, seq_len, d_model = hidden_states.shape
+    if batch <= 0 or seq_len <= 0 or batch * seq_len >= 2**31:
+        return False
+    if not supported_shape(d_model, num_heads):
+        return False
+    if weight.shape != (3 * d_model, d_model) or (bias is not None and bias.shape != (3 * d_model,)):
+        return False
+    if any(t.dtype != hidden_states.dtype for t in tensors):
+        return False
+    if not all(t.is_contiguous() for t in tensors):
+        return False
+    if hidden_states.data_ptr() % 16 or weight.data_ptr() % 16 or (bias is not None and bias.data_ptr() % 8):
+        return False
+    if not library_available():
+        return False
+    return is_gfx950(hidden_states.device)
+
+
+def prevalidated_hip_qkv_native_bhsd(
+    hidden_states: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    num_heads: int,
+    block_m: int = DEFAULT_BLOCK_M,
+    block_n: int = DEFAULT_BLOCK_N,
+    block_k: int = DEFAULT_BLOCK_K,
+    num_warps: int = DEFAULT_NUM_WARPS,
+    value_layout: str = "bhsd",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, str]:
+    """Project after the caller established eligibility (reference:
+    prevalidated_triton_qkv_native_bhsd, :170-230).  Returns (query, key,
+    value, marker) as [B, H, S, D/H] tensors; query and key contiguous, value
+    contiguous or the seq-contiguous view described in the module docstring."""
+
+    _validate_launch_config(block_m, block_n, block_k, num_warps)
+    if value_layout not in VALUE_LAYOUTS:
+        raise ValueError(f"unknown value layout {value_layout!r}; expected one of {sorted(VALUE_LAYOUTS)}")
+    # The kernel reads x as [B*S, D] rows and the packed weight as [3D, D]:
+    # anything else would be read wrongly, so it is refused, not computed.
+    if not can_use_hip_qkv_native_bhsd(
+        hidden_states,
+        weight,
+        bias,
+        num_heads=num_heads,
+        block_m=block_m,
+        block_n=block_n,
+        block_k=block_k,
+        num_warps=num_warps,
+    ):
+        raise RuntimeError("HIP QKV native-layout projection inputs are ineligible for the gfx950 kernel")
+    batch, seq_len, d_model = hidden_states.shape
+    head_dim = d_model // num_heads
+    shape = (batch, num_heads, seq_len, head_dim)
+    device, dtype = hidden_states.device, hidden_states.dtype
+    query = torch.empty(shape, device=device, dtype=dtype)
+    key = torch.empty_like(query)
+    if value_layout == "seq_major":
+        seq_stride = (seq_len + 7) // 8 * 8
+        storage = torch.empty((batch, num_heads, head_dim, seq_stride), device=device, dtype=dtype)
+        value = storage[..., :seq_len].transpose(-1, -2)
+    else:
+        seq_stride = 0
+        value = torch.empty_like(query)
+    try:
+        status = load_library().sah_qkv_projection(
+            hidden_states.data_ptr(),
+            weight.data_ptr(),
+            None if bias is None else bias.data_ptr(),
+            query.data_ptr(),
+            key.data_ptr(),
+            value.data_ptr(),
+            batch,
+            seq_len,
+            d_model,
+            num_heads,
+            hidden_states.stride(1),
+            VALUE_LAYOUTS[value_layout],
+            seq_stride,
+            dtype_code(dtype),
+            block_m,
+            block_n,
+            block_k,
+            num_warps,
+            stream_handle(device),
+        )
+        check_status(status, "sah_qkv_projection")
+    except Exception as exc:
+        raise RuntimeError("HIP QKV native-layout projection execution failed") from exc
+    return query, key, value, HIP_QKV_NATIVE_BHSD_BACKEND
+
+
+def hip_qkv_native_bhsd(
+    hidden_states: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    num_heads: int,
+    block_m: int = DEFAULT_BLOCK_M,
+    block_n: int = DEFAULT_BLOCK_N,
+    block_k: int = DEFAULT_BLOCK_K,
+    num_warps: int = DEFAULT_NUM_WARPS,
+    value_layout: str = "bhsd",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, str]:
+    """Strict entry (reference: triton_qkv_native_bhsd, :233-265): checks
+    eligibility first and raises RuntimeError "... ineligible" otherwise."""
+
+    _validate_launch_config(block_m, block_n, block_k, num_warps)
+    if not can_use_hip_qkv_native_bhsd(
+        hidden_states,
+        weight,
+        bias,
+        num_heads=num_heads,
+        block_m=block_m,
+        block_n=block_n,
+        block_k=block_k,
+        num_warps=num_warps,
+    ):
+        raise RuntimeError("HIP QKV native-layout projection is ineligible")
+    return prevalidated_hip_qkv_native_bhsd(
+        hidden_states,
+        weight,
+        bias,
+        num_heads=num_heads,
+        block_m=block_m,
+        block_n=block_n,
+        block_k=block_k,
+        num_warps=num_warps,
+        value_layout=value_layout,
+    )
+
+
+__all__ = [
+    "DEFAULT_BLOCK_K",
+    "DEFAULT_BLOCK_M",
+    "DEFAULT_BLOCK_N",
+    "DEFAULT_NUM_WARPS",
+    "HIP_QKV_NATIVE_BHSD_BACKEND",
+    "VALUE_LAYOUTS",
+    "can_use_hip_qkv_native_bhsd",
+    "hip_qkv_native_bhsd",
+    "hip_qkv_native_bhsd_available",
+    "launch_config_is_valid",
+    "prevalidated_hip_qkv_native_bhsd",
+    "supported_shape",
+]

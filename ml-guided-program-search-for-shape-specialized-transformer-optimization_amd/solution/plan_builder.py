@@ -141,6 +141,7 @@ class HardwareCapabilities:
     hip_initial_norm: bool = False
     hip_linear_exact_gelu: bool = False
     hip_exact_gelu: bool = False
+    hip_qkv_native_bhsd: bool = False
 
     @property
     def is_gfx950(self) -> bool:
@@ -189,6 +190,7 @@ class HardwareCapabilities:
             hip_initial_norm=hip_available,
             hip_linear_exact_gelu=hip_available,
             hip_exact_gelu=hip_available,
+            hip_qkv_native_bhsd=hip_available,
         )
 
 
@@ -324,8 +326,53 @@ class PlanBuilder:
         hardware: HardwareCapabilities,
         reject: Reject,
     ) -> None:
-        if config.program.qkv_materialization is QKVMaterialization.TRITON_NATIVE_BHSD:
+        materialization = config.program.qkv_materialization
+        if materialization is QKVMaterialization.TRITON_NATIVE_BHSD:
             _unavailable(reject, "program.qkv_materialization", "Triton native-layout QKV projection")
+            return
+        if materialization is not QKVMaterialization.HIP_NATIVE_BHSD:
+            return
+        # The reference's TRITON_NATIVE_BHSD branch (solution/plan_builder.py:381-446)
+        # for 16-bit models with native-dtype weights and this kernel's shapes.
+        from .kernels.projection.hip_qkv_layout import launch_config_is_valid, supported_shape
+
+        field = "program.qkv_materialization"
+        if not hardware.hip_qkv_native_bhsd:
+            reject("backend_unavailable", field, "the gfx950 HIP library is not loaded")
+        if context.device.type != "cuda" or not hardware.is_gfx950:
+            reject("requires_gfx950", field, "HIP kernels require an MI355X (gfx950) GPU")
+        if not context.inference:
+            reject("requires_inference", field, "native BHSD QKV is available only for inference")
+        if context.dtype not in {torch.float16, torch.bfloat16}:
+            reject("unsupported_dtype", field, "HIP native BHSD QKV runs on FP16 and BF16 models")
+        if config.program.qkv_projection is not ProjectionBackend.INPUT_DTYPE:
+            reject(
+                "backend_incompatible",
+                "program.qkv_projection",
+                "HIP native BHSD QKV multiplies the native-dtype packed weights",
+            )
+        if not supported_shape(context.d_model, context.num_heads):
+            reject(
+                "unsupported_shape",
+                field,
+                "HIP native BHSD QKV needs d_model % 256 == 0 and head_dim % 8 == 0",
+            )
+        if context.batch_size * context.seq_len >= 2**31:
+            reject("unsupported_shape", field, "HIP native BHSD QKV needs batch * seq_len < 2^31")
+        if config.schedule.runtime is RuntimeBackend.COMPILED_FORWARD:
+            reject(
+                "runtime_incompatible",
+                "schedule.runtime",
+                "native BHSD QKV is not nested in compiled forward",
+            )
+        launch = config.schedule.qkv_launch
+        assert launch is not None
+        if not launch_config_is_valid(launch.block_m, launch.block_n, launch.block_k, launch.num_warps):
+            reject(
+                "unsupported_launch_value",
+                "schedule.qkv_launch",
+                "HIP native BHSD QKV implements (256, 256, 64, 8)",
+            )
 
     # ---------------------------------------------------------------- attention
     @staticmethod

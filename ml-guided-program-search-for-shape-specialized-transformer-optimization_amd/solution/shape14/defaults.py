@@ -59,7 +59,10 @@ def conservative_streamed_config() -> ConfigSpec:
 
 
 def hip_streamed_config(
-    *, microbatch_size: int = DEFAULT_MICROBATCH_SIZE, ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU
+    *,
+    microbatch_size: int = DEFAULT_MICROBATCH_SIZE,
+    ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU,
+    qkv: QKVMaterialization = QKVMaterialization.VIEW,
 ) -> ConfigSpec:
     """The gfx950 long-sequence program with ordered microbatches."""
 
@@ -67,6 +70,7 @@ def hip_streamed_config(
         microbatch_size=microbatch_size,
         attention_launch=HIP_LONG_SEQUENCE_ATTENTION_LAUNCH,
         ffn=ffn,
+        qkv=qkv,
     )
 
 

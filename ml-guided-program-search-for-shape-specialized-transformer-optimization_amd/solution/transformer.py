@@ -304,22 +304,56 @@ class _SelfAttention(nn.Module):
         observation: _ExecutionObservation | None,
     ) -> torch.Tensor:
         batch, seq, _ = value.shape
-        packed = self.qkv_proj.forward_backend(value, plan.qkv_projection_backend)
-        query, key, projected = split_qkv(
-            packed,
-            self.num_heads,
-            contiguous=plan.qkv_materialization is QKVMaterialization.CONTIGUOUS,
-        )
-        if observation is not None:
-            storage = packed.untyped_storage().data_ptr()
-            shares = all(t.untyped_storage().data_ptr() == storage for t in (query, key, projected))
-            actual = QKVMaterialization.VIEW if shares else QKVMaterialization.CONTIGUOUS
-            if actual is not plan.qkv_materialization:
-                raise RuntimeError("QKV materialization does not match the plan")
-            observation.qkv_materializations.append(actual.value)
-            observation.qkv_launches.append(_launch_dict(plan.qkv_launch))
-
         backend = plan.attention_backend
+        if plan.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD:
+            # The reference's native-layout branch (solution/transformer.py:384-431):
+            # the projection kernel writes head-major Q / K / V itself.  The HIP
+            # attention reads V^T, so V is written seq-contiguous for it.
+            from .kernels.projection.hip_qkv_layout import (
+                HIP_QKV_NATIVE_BHSD_BACKEND,
+                prevalidated_hip_qkv_native_bhsd,
+            )
+
+            launch = plan.qkv_launch
+            if launch is None:
+                raise RuntimeError("HIP native-layout QKV plan is missing launch parameters")
+            query, key, projected, marker = prevalidated_hip_qkv_native_bhsd(
+                value,
+                self.qkv_proj.weight,
+                self.qkv_proj.bias,
+                num_heads=self.num_heads,
+                block_m=launch.block_m,
+                block_n=launch.block_n,
+                block_k=launch.block_k,
+                num_warps=launch.num_warps,
+                value_layout="seq_major" if backend is AttentionBackend.HIP_STREAMING_DH64 else "bhsd",
+            )
+            _strict_backend_marker(
+                marker,
+                expected_marker=HIP_QKV_NATIVE_BHSD_BACKEND,
+                planned_backend=plan.qkv_materialization.value,
+            )
+            qkv_dtype = query.dtype
+            if observation is not None:
+                observation.qkv_materializations.append(plan.qkv_materialization.value)
+                observation.qkv_launches.append(_launch_dict(plan.qkv_launch))
+        else:
+            packed = self.qkv_proj.forward_backend(value, plan.qkv_projection_backend)
+            qkv_dtype = packed.dtype
+            query, key, projected = split_qkv(
+                packed,
+                self.num_heads,
+                contiguous=plan.qkv_materialization is QKVMaterialization.CONTIGUOUS,
+            )
+            if observation is not None:
+                storage = packed.untyped_storage().data_ptr()
+                shares = all(t.untyped_storage().data_ptr() == storage for t in (query, key, projected))
+                actual = QKVMaterialization.VIEW if shares else QKVMaterialization.CONTIGUOUS
+                if actual is not plan.qkv_materialization:
+                    raise RuntimeError("QKV materialization does not match the plan")
+                observation.qkv_materializations.append(actual.value)
+                observation.qkv_launches.append(_launch_dict(plan.qkv_launch))
+
         if backend is AttentionBackend.HIP_STREAMING_DH64:
             from .shape14.hip_streaming_dh64 import (
                 HIP_STREAMING_DH64_CAUSAL_ATTENTION_BSD_BACKEND,
@@ -375,7 +409,7 @@ class _SelfAttention(nn.Module):
                 else _dtype_name(query.dtype)
             )
             observation.qkv_projection_backends.append(plan.qkv_projection_backend.value)
-            observation.qkv_projection_compute_dtypes.append(_dtype_name(packed.dtype))
+            observation.qkv_projection_compute_dtypes.append(_dtype_name(qkv_dtype))
             observation.attention_output_layouts.append(layout.value)
             observation.attention_output_bridges.append(plan.attention_output_bridge.value)
             observation.attention_output_projection_backends.append(

@@ -126,6 +126,67 @@ def test_fused_ffn_input_plan_matches_the_bf16_reference_path(gpu_device, shape,
     assert observed["ffn_backend"] == ffn_backend
 
 
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 256, 512, 8, 2048, 2),   # BASELINE config 2 widths
+        (1, 300, 1024, 16, 4096, 2),  # long-sequence widths, ragged length
+        (2, 128, 2048, 32, 8192, 1),  # config 4 widths
+    ],
+)
+def test_native_qkv_plan_matches_the_bf16_reference_path(gpu_device, shape):
+    """The program whose QKV projection writes head-major Q / K and the
+    seq-contiguous V^T straight from its epilogue, end to end against the
+    official bf16 path."""
+
+    from solution.config import QKVMaterialization, hip_config
+
+    batch, seq, width, heads, ffn, layers = shape
+    print(f"native qkv model parity {shape}", flush=True)
+    config = TransformerConfig(batch, seq, width, heads, ffn, layers, True)
+    state = xavier_init_weights(config, seed=2468)
+    x = generate_input(config, seed=2468).to(torch.bfloat16)
+    model = _model(config, state, gpu_device, torch.bfloat16)
+    model.configure_execution(config=hip_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD))
+    model.set_execution_observation(True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    torch.cuda.synchronize()
+    reference = forward(cast_state(state, torch.bfloat16), x, config)
+    exact = forward(cast_state(cast_state(state, torch.bfloat16), torch.float32), x.float(), config)
+    _check_bf16_model(exact, reference.float(), output, f"native qkv model {shape}")
+    description = model.describe_execution_path()
+    observed = description["observed_execution_signature"]
+    assert observed == description["expected_execution_signature"]
+    assert observed["qkv_materialization"] == "hip_native_bhsd"
+
+
+def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
+    """The graph-replay runtime with both fused GEMM epilogues (native-layout
+    QKV and Linear + exact GELU): several replays with new inputs, eager work
+    and synchronizations between them, each bitwise equal to the eager
+    program on the same input."""
+
+    from solution.config import FFNBackend, QKVMaterialization, hip_config
+
+    config = TransformerConfig(4, 256, 512, 8, 2048, 2, True)
+    state = xavier_init_weights(config, seed=13)
+    options = dict(ffn=FFNBackend.HIP_LINEAR_EXACT_GELU, qkv=QKVMaterialization.HIP_NATIVE_BHSD)
+    graph_model = _model(config, state, gpu_device, torch.bfloat16)
+    graph_model.configure_execution(config=hip_config(graph=True, **options))
+    eager_model = _model(config, state, gpu_device, torch.bfloat16)
+    eager_model.configure_execution(config=hip_config(**options))
+    with torch.inference_mode():
+        for seed in (1, 2, 3):
+            print(f"fused graph replay input seed {seed}", flush=True)
+            x = generate_input(config, seed=seed).to(torch.bfloat16).to(gpu_device)
+            replayed = graph_model(x)
+            torch.cuda.synchronize()
+            expected = eager_model(x)
+            torch.cuda.synchronize()
+            assert torch.equal(replayed, expected), f"replay {seed} differs from eager"
+
+
 def test_streamed_output_equals_its_chunks_bitwise(gpu_device):
     """The streamed driver runs ordered chunks and writes each chunk's final
     norm into the logical output: identical to running the chunks alone."""

@@ -149,3 +149,45 @@ def test_gelu_entry_validates_before_launch():
     assert library.sah_gelu(fake, fake, 0, 2, 4096, 4, None) == _library.SAH_OK
     status = library.sah_gelu(ctypes.c_void_p(4096 + 2), fake, 10, 2, 4096, 4, None)
     assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()
+
+
+def test_qkv_projection_entry_validates_before_launch():
+    """sah_qkv_projection's launch table and argument checks (no kernel runs)."""
+
+    from solution.kernels.projection.hip_qkv_layout import launch_config_is_valid, supported_shape
+
+    library = _library.load_library()
+    assert library.sah_qkv_launch_supported(256, 256, 64, 8) == 1
+    assert launch_config_is_valid(256, 256, 64, 8)
+    for launch in [(64, 32, 32, 4), (128, 256, 64, 8), (256, 256, 32, 8), (256, 256, 64, 4)]:
+        assert library.sah_qkv_launch_supported(*launch) == 0
+        assert not launch_config_is_valid(*launch)
+    assert not launch_config_is_valid(256, 256, 64, True)
+    # d_model a multiple of 256, head_dim a multiple of 8
+    assert supported_shape(1024, 16) and supported_shape(512, 8) and supported_shape(2048, 32)
+    assert not supported_shape(32, 4) and not supported_shape(640, 10) and not supported_shape(1024, 256)
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    base = dict(batch=2, seq=100, d=1024, heads=16, ldx=1024, layout=_library.SAH_QKV_VALUE_SEQ_MAJOR,
+                ldv=104, dtype=2, launch=(256, 256, 64, 8))
+
+    def call(x=fake, **over):
+        a = {**base, **over}
+        return library.sah_qkv_projection(x, fake, None, fake, fake, fake, a["batch"], a["seq"], a["d"],
+                                          a["heads"], a["ldx"], a["layout"], a["ldv"], a["dtype"],
+                                          *a["launch"], None)
+
+    assert call(launch=(64, 32, 32, 4)) == _library.SAH_ERR_UNSUPPORTED
+    assert call(dtype=0) == _library.SAH_ERR_UNSUPPORTED
+    assert call(d=640, heads=10, ldx=640) == _library.SAH_ERR_UNSUPPORTED and b"multiple" in library.sah_last_error()
+    assert call(heads=256) == _library.SAH_ERR_UNSUPPORTED  # head_dim 4
+    assert call(layout=7) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ldv=96) == _library.SAH_ERR_INVALID_ARGUMENT  # below seq_len
+    assert call(ldv=101) == _library.SAH_ERR_INVALID_ARGUMENT  # not a multiple of 8
+    assert call(ldx=1000) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(batch=-1) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(seq=0) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(batch=40000, seq=100000, ldv=100000) == _library.SAH_ERR_UNSUPPORTED  # 4e9 tokens
+    assert call(batch=0) == _library.SAH_OK  # nothing to do, nothing launched
+    assert call(layout=_library.SAH_QKV_VALUE_BHSD, ldv=0, batch=0) == _library.SAH_OK
+    status = call(x=ctypes.c_void_p(4096 + 8))
+    assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()

@@ -56,6 +56,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         hip_initial_norm=True,
         hip_linear_exact_gelu=True,
         hip_exact_gelu=True,
+        hip_qkv_native_bhsd=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -395,3 +396,73 @@ def test_elementwise_gelu_plans_and_rejections():
     assert ("program.ffn", "backend_unavailable") in codes(unavailable)
     with pytest.raises(ValueError, match="not part of the gfx950 program"):
         hip_config(ffn=FFNBackend.TRITON_EXACT_GELU)
+
+
+def test_native_qkv_plans_and_rejections():
+    """The HIP native-layout QKV projection: accepted for 16-bit inference on
+    gfx950 with its launch, rejected with structured reasons otherwise (the
+    reference's TRITON_NATIVE_BHSD rules, solution/plan_builder.py:381-446)."""
+
+    import dataclasses
+
+    from solution.config import (
+        HIP_QKV_LAUNCH,
+        PrecisionPlan,
+        ProjectionBackend,
+        QKVLaunchParams,
+        QKVMaterialization,
+        RuntimeBackend,
+    )
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    native = hip_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD)
+    assert native.program.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD
+    assert native.schedule.qkv_launch == HIP_QKV_LAUNCH == QKVLaunchParams(256, 256, 64, 8)
+    assert ConfigSpec.from_dict(native.to_dict()) == native
+    assert native.config_id != hip_config().config_id
+    plan = builder.build(native, _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4), _gfx950())
+    assert plan.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD
+    assert plan.expected_trace.to_dict()["qkv_materialization"] == "hip_native_bhsd"
+    streamed = builder.build(hip_streamed_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD), _context(), _gfx950())
+    assert streamed.use_streamed_execution and streamed.qkv_launch == HIP_QKV_LAUNCH
+    # the launch is part of the schedule exactly when a native materialization is selected
+    with pytest.raises(ValueError, match="qkv_launch"):
+        dataclasses.replace(native, schedule=dataclasses.replace(native.schedule, qkv_launch=None))
+    with pytest.raises(ValueError, match="qkv_launch"):
+        dataclasses.replace(hip_config(), schedule=dataclasses.replace(hip_config().schedule, qkv_launch=HIP_QKV_LAUNCH))
+    with pytest.raises(ValueError, match="not part of the gfx950 program"):
+        hip_config(qkv=QKVMaterialization.CONTIGUOUS)
+    unavailable = builder.evaluate(native, _context(), _gfx950(hip_qkv_native_bhsd=False))
+    assert ("program.qkv_materialization", "backend_unavailable") in codes(unavailable)
+    not_gfx950 = builder.evaluate(native, _context(), _gfx950(gcn_arch="gfx942"))
+    assert ("program.qkv_materialization", "requires_gfx950") in codes(not_gfx950)
+    odd_width = builder.evaluate(native, _context(d=640, heads=10, ffn=2560), _gfx950())
+    assert ("program.qkv_materialization", "unsupported_shape") in codes(odd_width)
+    fp32 = builder.evaluate(native, _context(dtype=torch.float32), _gfx950())
+    assert ("program.qkv_materialization", "unsupported_dtype") in codes(fp32)
+    shadow = dataclasses.replace(
+        native,
+        program=dataclasses.replace(
+            native.program,
+            precision_plan=PrecisionPlan.FP16_QKV_ATTENTION,
+            qkv_projection=ProjectionBackend.FP16_SHADOW,
+        ),
+    )
+    assert ("program.qkv_projection", "backend_incompatible") in codes(builder.evaluate(shadow, _context(), _gfx950()))
+    wrong_launch = dataclasses.replace(
+        native, schedule=dataclasses.replace(native.schedule, qkv_launch=QKVLaunchParams(64, 32, 32, 4))
+    )
+    assert ("schedule.qkv_launch", "unsupported_launch_value") in codes(builder.evaluate(wrong_launch, _context(), _gfx950()))
+    compiled = dataclasses.replace(
+        native,
+        schedule=dataclasses.replace(native.schedule, runtime=RuntimeBackend.COMPILED_FORWARD, compile_mode="max-autotune"),
+    )
+    assert ("schedule.runtime", "runtime_incompatible") in codes(builder.evaluate(compiled, _context(), _gfx950()))
+    training = builder.evaluate(native, _context(grad=True), _gfx950())
+    assert ("program.qkv_materialization", "requires_inference") in codes(training)
+    # the reference's Triton materialization stays unavailable, not replaced
+    triton = dataclasses.replace(
+        native, program=dataclasses.replace(native.program, qkv_materialization=QKVMaterialization.TRITON_NATIVE_BHSD)
+    )
+    assert ("program.qkv_materialization", "backend_unavailable") in codes(builder.evaluate(triton, _context(), _gfx950()))
