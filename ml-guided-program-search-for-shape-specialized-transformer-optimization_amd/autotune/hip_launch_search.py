@@ -16,7 +16,9 @@ build:
 * it is a coordinate search: attention launch, then norm launch, then the FFN
   activation path (hipBLASLt + torch GELU, hipBLASLt + the HIP elementwise
   GELU, or the fused HIP Linear + exact-GELU kernel where the plan builder
-  accepts it), then runtime, each stage keeping the best of the previous ones; a stage replaces the
+  accepts it), then the QKV path (hipBLASLt packed projection with zero-copy
+  views, or the HIP projection writing head-major Q / K and the attention's
+  V^T layout), then runtime, each stage keeping the best of the previous ones; a stage replaces the
   current choice only when a candidate is faster by more than ``min_gain``
   (1% by default), because repeated timings of one program differ by a few
   tenths of a percent and a noise-level "win" is not a reason to deploy a
@@ -58,10 +60,12 @@ import torch
 from solution.config import (
     HIP_GELU_LAUNCH,
     HIP_LINEAR_LAUNCH,
+    HIP_QKV_LAUNCH,
     AttentionLaunchParams,
     ConfigSpec,
     FFNBackend,
     NormLaunchParams,
+    QKVMaterialization,
     RuntimeBackend,
     hip_config,
 )
@@ -148,6 +152,23 @@ def _ffn_variants(config: ConfigSpec) -> list[ConfigSpec]:
         with_ffn(FFNBackend.TORCH),
         with_ffn(FFNBackend.HIP_EXACT_GELU, ffn_launch=HIP_GELU_LAUNCH),
         with_ffn(FFNBackend.HIP_LINEAR_EXACT_GELU, ffn_input_launch=HIP_LINEAR_LAUNCH),
+    ]
+
+
+def _qkv_variants(config: ConfigSpec) -> list[ConfigSpec]:
+    """The QKV paths: hipBLASLt's packed projection viewed as Q / K / V, or
+    the HIP projection with the head-major epilogue, each with its launch."""
+
+    def with_qkv(materialization: QKVMaterialization, launch=None) -> ConfigSpec:
+        return dataclasses.replace(
+            config,
+            program=dataclasses.replace(config.program, qkv_materialization=materialization),
+            schedule=dataclasses.replace(config.schedule, qkv_launch=launch),
+        )
+
+    return [
+        with_qkv(QKVMaterialization.VIEW),
+        with_qkv(QKVMaterialization.HIP_NATIVE_BHSD, HIP_QKV_LAUNCH),
     ]
 
 
@@ -262,7 +283,8 @@ class HipLaunchSearch:
             launch = config.schedule.attention_launch
             self.log(
                 f"{config.config_id[:16]} attention {launch.to_dict() if launch else None} "
-                f"norm {config.schedule.residual_norm_launch.to_dict()} runtime "
+                f"norm {config.schedule.residual_norm_launch.to_dict()} ffn {config.program.ffn.value} "
+                f"qkv {config.program.qkv_materialization.value} runtime "
                 f"{config.schedule.runtime.value}/{config.schedule.microbatch_size}: {ms:.5g} ms/sequence"
             )
             if config.config_id == current.config_id:
@@ -285,6 +307,7 @@ class HipLaunchSearch:
         base = self._best([_with_attention(base, launch) for launch in ATTENTION_LAUNCHES], timed, base).config
         base = self._best([_with_norms(base, launch) for launch in NORM_LAUNCHES], timed, base).config
         base = self._best(_ffn_variants(base), timed, base).config
+        base = self._best(_qkv_variants(base), timed, base).config
         winner = self._best(
             _runtime_variants(base, streamed=self.streamed, batch=math.gcd(self.shape.batch_size, self.timed)),
             timed,

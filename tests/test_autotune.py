@@ -15,6 +15,7 @@ from autotune.hip_launch_search import (
     HipLaunchSearch,
     SearchShape,
     _ffn_variants,
+    _qkv_variants,
     _runtime_variants,
     _with_attention,
     _with_norms,
@@ -33,6 +34,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         triton_mixed_residual_norm=False, triton_initial_norm=False, triton_exact_gelu=False,
         triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
         hip_residual_norm=True, hip_initial_norm=True, hip_exact_gelu=True, hip_linear_exact_gelu=True,
+        hip_qkv_native_bhsd=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -143,3 +145,23 @@ def test_ffn_stage_offers_hipblaslt_and_the_fused_kernel():
     )
     assert no_kernel.legal(variants[0], device)
     assert not no_kernel.legal(variants[1], device) and not no_kernel.legal(variants[2], device)
+
+
+def test_qkv_stage_offers_views_and_the_native_layout_kernel():
+    from solution.config import HIP_QKV_LAUNCH, QKVMaterialization
+
+    for workload in ("c2", "c4", "c5"):
+        shape = SearchShape(*WORKLOADS[workload])
+        search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
+        base = search.incumbent()
+        variants = _qkv_variants(base)
+        assert [v.program.qkv_materialization for v in variants] == [
+            QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD,
+        ]
+        assert variants[0] == base  # the default program is one of them
+        assert variants[1].schedule.qkv_launch == HIP_QKV_LAUNCH
+        device = torch.device("cuda")
+        assert all(search.legal(v, device) for v in variants), workload
+    # without the kernel the native variant is rejected, never timed
+    no_kernel = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_qkv_native_bhsd=False))
+    assert no_kernel.legal(variants[0], device) and not no_kernel.legal(variants[1], device)
