@@ -25,7 +25,8 @@ profiles/attn_fwd_c5_chunk_traffic.md as ``key = value`` lines and is
 reported only while ``source_digest`` there equals the digest of the current
 attention source and default launch (otherwise null).
 
-``--kernel attention|norm|copy|linear|linear-torch|gelu|gelu-torch|qkv|qkv-torch`` runs one kernel alone at
+``--kernel attention|norm|copy|linear|linear-torch|gelu|gelu-torch|qkv|qkv-torch|boundary|boundary-torch|``
+``boundary-ffn|boundary-ffn-torch`` runs one kernel alone at
 the workload's per-chunk shape (for rocprofv3 runs) and prints each launch's
 duration: attention over a packed [2, S, 3D] QKV view exactly as the model
 hands it over, the fused residual+LayerNorm at one chunk's block boundary, a
@@ -35,7 +36,10 @@ the same projection as hipBLASLt F.linear followed by torch's exact GELU, or
 the exact GELU alone on the [2S, F] hidden tensor (HIP in place, or torch), or
 the packed QKV projection ([2S, D] -> 3 x [2, H, S, 64]): the HIP kernel with
 the head-major epilogue and seq-contiguous value, or hipBLASLt F.linear into
-the packed [2S, 3D] tensor the default program views.  Attention runs with
+the packed [2S, 3D] tensor the default program views, or a residual boundary
+with its projection: the fused HIP Linear + residual + LayerNorm kernel, or
+hipBLASLt F.linear followed by the HIP residual LayerNorm, for the attention
+output projection (D -> D) or the FFN output projection (F -> D).  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 """
 
@@ -345,6 +349,23 @@ def kernel_alone(kind: str, repeat: int) -> int:
             else:
                 run = lambda: torch.nn.functional.linear(x, weight, bias)
             work = f"{2 * batch * seq * width * 3 * width / 1e12:.3f} TFLOP per launch"
+        elif kind.startswith("boundary"):
+            from solution.kernels.boundary import block_rows_for, hip_linear_residual_norm
+
+            in_features = w["ffn_dim"] if kind.startswith("boundary-ffn") else width
+            x = torch.randn(batch, seq, in_features, generator=generator, device=device, dtype=torch.bfloat16)
+            bound = math.sqrt(6.0 / (width + in_features))
+            weight = ((torch.rand(width, in_features, generator=generator, device=device) * 2 - 1) * bound).to(torch.bfloat16)
+            bias = torch.zeros(width, device=device, dtype=torch.bfloat16)
+            value = torch.randn(batch, seq, width, generator=generator, device=device, dtype=torch.bfloat16)
+            layer_norm = torch.nn.LayerNorm(width).to(device=device, dtype=torch.bfloat16)
+            if kind.endswith("-torch"):
+                run = lambda: hip_residual.hip_residual_layer_norm(
+                    value, torch.nn.functional.linear(x, weight, bias), layer_norm)
+            else:
+                run = lambda: hip_linear_residual_norm(
+                    x, weight, bias, value, layer_norm, block_rows=block_rows_for(width), num_warps=8)
+            work = f"{2 * batch * seq * in_features * width / 1e12:.3f} TFLOP + {8 * batch * seq * width / 1e9:.3f} GB per launch"
         elif kind in ("gelu", "gelu-torch"):
             from solution.kernels.ffn import prevalidated_hip_exact_gelu
 
@@ -425,7 +446,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
-                                             "qkv", "qkv-torch"),
+                                             "qkv", "qkv-torch", "boundary", "boundary-torch", "boundary-ffn",
+                                             "boundary-ffn-torch"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()

@@ -246,6 +246,42 @@ int sah_qkv_projection(
  * solution/kernels/projection/triton_qkv_layout.py:29-43). */
 int sah_qkv_launch_supported(int block_m, int block_n, int block_k, int num_warps);
 
+/*
+ * Fused Linear + residual add + LayerNorm / RMSNorm boundary:
+ *   update     = round_to(dtype, x weight^T + bias)   (fp32 accumulation, bias in fp32)
+ *   residual   = round_to(dtype, value + update)
+ *   normalized = round_to(dtype, norm(residual) * gamma + beta)
+ * The update never reaches HBM.  The residual and norm arithmetic are those
+ * of sah_residual_norm (statistics in fp32 over the rounded residual).
+ *
+ * Replaces the reference's
+ *   _linear_residual_norm_kernel + triton_linear_residual_norm
+ *     (solution/kernels/boundary/triton_linear_residual_norm.py:34-109, 197-245)
+ *   the out_proj / ffn_out projection + _apply_residual_norm pair of the
+ *   default path (solution/transformer.py:727-730, 1515-1644)
+ * x: [rows, in_features] with row stride x_row_stride; weight: [width,
+ * in_features] contiguous; bias, gamma, beta: [width] or NULL (0, 1, 0);
+ * value, residual, normalized: [rows, width] contiguous, residual and
+ * normalized not aliasing any input.  Shared dtype SAH_DTYPE_BF16 or
+ * SAH_DTYPE_F16; norm_kind SAH_NORM_LAYER or SAH_NORM_RMS.  width 512 or
+ * 1024, in_features a multiple of 64, x_row_stride a multiple of 8; tensors
+ * 16-byte aligned, bias 8-byte.  Launch: block_rows = 65536 / width whole rows
+ * per workgroup of num_warps = 8 wavefronts, see
+ * sah_linear_residual_norm_launch_supported().
+ */
+int sah_linear_residual_norm(
+    const void* x, const void* weight, const void* bias,
+    const void* value, const void* gamma, const void* beta,
+    void* residual, void* normalized,
+    int64_t rows, int64_t in_features, int64_t width, int64_t x_row_stride,
+    float eps, int dtype, int norm_kind, int block_rows, int num_warps,
+    sah_stream_t stream);
+
+/* 1 if sah_linear_residual_norm implements (width, block_rows, num_warps),
+ * else 0 (mirrors the reference's _launch_is_valid,
+ * solution/kernels/boundary/triton_linear_residual_norm.py:114-119). */
+int sah_linear_residual_norm_launch_supported(int64_t width, int block_rows, int num_warps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,7 +18,10 @@ build:
   GELU, or the fused HIP Linear + exact-GELU kernel where the plan builder
   accepts it), then the QKV path (hipBLASLt packed projection with zero-copy
   views, or the HIP projection writing head-major Q / K and the attention's
-  V^T layout), then runtime, each stage keeping the best of the previous ones; a stage replaces the
+  V^T layout), then the residual boundary (hipBLASLt output projections
+  followed by the HIP residual norm, or the fused HIP Linear + residual +
+  LayerNorm boundary where the plan builder accepts it), then runtime, each
+  stage keeping the best of the previous ones; a stage replaces the
   current choice only when a candidate is faster by more than ``min_gain``
   (1% by default), because repeated timings of one program differ by a few
   tenths of a percent and a noise-level "win" is not a reason to deploy a
@@ -66,8 +69,10 @@ from solution.config import (
     FFNBackend,
     NormLaunchParams,
     QKVMaterialization,
+    ResidualNormBackend,
     RuntimeBackend,
     hip_config,
+    hip_linear_boundary_launch,
 )
 from solution.plan import ExecutionContext
 from solution.plan_builder import HardwareCapabilities, PlanBuilder
@@ -170,6 +175,18 @@ def _qkv_variants(config: ConfigSpec) -> list[ConfigSpec]:
         with_qkv(QKVMaterialization.VIEW),
         with_qkv(QKVMaterialization.HIP_NATIVE_BHSD, HIP_QKV_LAUNCH),
     ]
+
+
+def _boundary_variants(config: ConfigSpec, d_model: int) -> list[ConfigSpec]:
+    """The residual boundaries: the current one, and the output projections
+    fused into them (with the width's launch; the initial norm keeps its own)."""
+
+    fused = dataclasses.replace(
+        config,
+        program=dataclasses.replace(config.program, residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED),
+        schedule=dataclasses.replace(config.schedule, residual_norm_launch=hip_linear_boundary_launch(d_model)),
+    )
+    return [config, fused]
 
 
 def _with_norms(config: ConfigSpec, launch: NormLaunchParams) -> ConfigSpec:
@@ -284,7 +301,8 @@ class HipLaunchSearch:
             self.log(
                 f"{config.config_id[:16]} attention {launch.to_dict() if launch else None} "
                 f"norm {config.schedule.residual_norm_launch.to_dict()} ffn {config.program.ffn.value} "
-                f"qkv {config.program.qkv_materialization.value} runtime "
+                f"qkv {config.program.qkv_materialization.value} "
+                f"boundary {config.program.residual_norm.value} runtime "
                 f"{config.schedule.runtime.value}/{config.schedule.microbatch_size}: {ms:.5g} ms/sequence"
             )
             if config.config_id == current.config_id:
@@ -308,6 +326,7 @@ class HipLaunchSearch:
         base = self._best([_with_norms(base, launch) for launch in NORM_LAUNCHES], timed, base).config
         base = self._best(_ffn_variants(base), timed, base).config
         base = self._best(_qkv_variants(base), timed, base).config
+        base = self._best(_boundary_variants(base, self.shape.d_model), timed, base).config
         winner = self._best(
             _runtime_variants(base, streamed=self.streamed, batch=math.gcd(self.shape.batch_size, self.timed)),
             timed,

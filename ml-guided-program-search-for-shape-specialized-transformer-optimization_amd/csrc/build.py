@@ -24,7 +24,14 @@ PACKAGE_ROOT = CSRC.parent
 LIB_DIR = PACKAGE_ROOT / "lib"
 BUILD_DIR = CSRC / "_build"
 LIBRARY_NAME = "libshape_aware_hip.so"
-SOURCES = ("capi.hip", "residual_norm.hip", "attention_fwd.hip", "linear_gelu.hip", "gelu.hip")
+SOURCES = (
+    "capi.hip",
+    "residual_norm.hip",
+    "attention_fwd.hip",
+    "linear_gelu.hip",
+    "gelu.hip",
+    "linear_norm.hip",
+)
 OFFLOAD_ARCH = "gfx950"
 
 HIPCC_FLAGS = (

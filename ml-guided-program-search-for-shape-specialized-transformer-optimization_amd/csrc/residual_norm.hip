@@ -38,25 +38,6 @@ struct VecIO {
   }
 };
 
-// Merge Welford states of equal count across the wavefront (butterfly, so
-// every lane ends with the row statistics).
-__device__ __forceinline__ void wave_welford(float& mean, float& m2, float count) {
-#pragma unroll
-  for (int offset = 1; offset < kWave; offset <<= 1) {
-    const float other_mean = __shfl_xor(mean, offset);
-    const float other_m2 = __shfl_xor(m2, offset);
-    const float delta = other_mean - mean;
-    mean = 0.5f * (mean + other_mean);
-    m2 = m2 + other_m2 + delta * delta * (0.5f * count);
-    count *= 2.0f;
-  }
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int offset = 1; offset < kWave; offset <<= 1) v += __shfl_xor(v, offset);
-  return v;
-}
 
 // TX: residual-stream dtype (value in, residual out); TU: update dtype;
 // TY: normalized dtype; TP: weight/bias dtype.  ITERS * 64 * VEC == width.

@@ -119,6 +119,27 @@ __device__ __forceinline__ u32x4 pack8(const float* in) {
   return __builtin_bit_cast(u32x4, v);
 }
 
+// Row statistics across a wavefront (the fused norms).
+// Merge Welford states of equal count across the wavefront (butterfly, so
+// every lane ends with the row statistics).
+__device__ __forceinline__ void wave_welford(float& mean, float& m2, float count) {
+#pragma unroll
+  for (int offset = 1; offset < 64; offset <<= 1) {
+    const float other_mean = __shfl_xor(mean, offset);
+    const float other_m2 = __shfl_xor(m2, offset);
+    const float delta = other_mean - mean;
+    mean = 0.5f * (mean + other_mean);
+    m2 = m2 + other_m2 + delta * delta * (0.5f * count);
+    count *= 2.0f;
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 1; offset < 64; offset <<= 1) v += __shfl_xor(v, offset);
+  return v;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline bool aligned16(const void* p) {

@@ -106,6 +106,7 @@ class ResidualNormBackend(_StrEnum):
     TRITON_LINEAR_MIXED = "triton_linear_mixed"
     HIP_FUSED = "hip_fused"
     HIP_MIXED = "hip_mixed"
+    HIP_LINEAR_FUSED = "hip_linear_fused"
 
 
 class InitialNormBackend(_StrEnum):
@@ -141,7 +142,16 @@ LAUNCHED_ATTENTION_BACKENDS = TRITON_ATTENTION_BACKENDS | HIP_ATTENTION_BACKENDS
 # Backends that write [B, S, H*Dh] directly.
 DIRECT_BSD_ATTENTION_BACKENDS = LAUNCHED_ATTENTION_BACKENDS
 HIP_RESIDUAL_NORM_BACKENDS = frozenset(
-    {ResidualNormBackend.HIP_FUSED, ResidualNormBackend.HIP_MIXED}
+    {
+        ResidualNormBackend.HIP_FUSED,
+        ResidualNormBackend.HIP_MIXED,
+        ResidualNormBackend.HIP_LINEAR_FUSED,
+    }
+)
+# Backends that fuse the branch's output projection into the residual
+# boundary (the update never reaches HBM).
+LINEAR_BOUNDARY_RESIDUAL_NORM_BACKENDS = frozenset(
+    {ResidualNormBackend.TRITON_LINEAR_MIXED, ResidualNormBackend.HIP_LINEAR_FUSED}
 )
 LAUNCHED_RESIDUAL_NORM_BACKENDS = frozenset(
     {
@@ -667,6 +677,14 @@ HIP_GELU_LAUNCH = FFNLaunchParams(block_size=4096, num_warps=8)
 HIP_QKV_LAUNCH = QKVLaunchParams(block_m=256, block_n=256, block_k=64, num_warps=8)
 
 
+def hip_linear_boundary_launch(d_model: int) -> NormLaunchParams:
+    """The launch of the HIP Linear + residual + LayerNorm boundary
+    (csrc/linear_norm.hip) for a model width: 65536 / d_model whole rows per
+    workgroup of 8 wavefronts."""
+
+    return NormLaunchParams(block_rows=max(1, 65536 // d_model), num_warps=8)
+
+
 def hip_config(
     *,
     microbatch_size: int | None = None,
@@ -675,6 +693,8 @@ def hip_config(
     norm_launch: NormLaunchParams = HIP_DEFAULT_NORM_LAUNCH,
     ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU,
     qkv: QKVMaterialization = QKVMaterialization.VIEW,
+    residual_norm: ResidualNormBackend = ResidualNormBackend.HIP_FUSED,
+    boundary_launch: NormLaunchParams | None = None,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
     norms and HIP initial norm, projections in the model dtype on hipBLASLt,
@@ -685,7 +705,12 @@ def hip_config(
     HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU).  ``qkv``
     picks how Q, K and V are produced: VIEW (hipBLASLt packed projection and
     zero-copy views) or HIP_NATIVE_BHSD (the HIP projection writing
-    head-major Q / K and a seq-contiguous V straight from its epilogue)."""
+    head-major Q / K and a seq-contiguous V straight from its epilogue).
+    ``residual_norm`` picks the boundary: HIP_FUSED (residual + norm after the
+    hipBLASLt output projections, with ``norm_launch``) or HIP_LINEAR_FUSED
+    (each output projection fused into its boundary, with ``boundary_launch``,
+    see hip_linear_boundary_launch); the initial norm always uses
+    ``norm_launch``."""
 
     ffn = FFNBackend(ffn)
     if ffn not in {FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU}:
@@ -693,6 +718,17 @@ def hip_config(
     qkv = QKVMaterialization(qkv)
     if qkv not in {QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD}:
         raise ValueError(f"QKV materialization {qkv.value!r} is not part of the gfx950 program")
+    residual_norm = ResidualNormBackend(residual_norm)
+    if residual_norm is ResidualNormBackend.HIP_LINEAR_FUSED:
+        if boundary_launch is None:
+            raise ValueError("the linear boundary needs boundary_launch (hip_linear_boundary_launch(d_model))")
+        residual_launch = boundary_launch
+    elif residual_norm is ResidualNormBackend.HIP_FUSED:
+        if boundary_launch is not None:
+            raise ValueError("boundary_launch is only for the linear boundary")
+        residual_launch = norm_launch
+    else:
+        raise ValueError(f"residual norm {residual_norm.value!r} is not part of the gfx950 program")
 
     if graph and microbatch_size is not None:
         raise ValueError("the graph runtime and the streamed schedule are exclusive")
@@ -711,14 +747,14 @@ def hip_config(
             qkv_materialization=qkv,
             attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
             ffn=ffn,
-            residual_norm=ResidualNormBackend.HIP_FUSED,
+            residual_norm=residual_norm,
             initial_norm=InitialNormBackend.HIP,
         ),
         schedule=ScheduleConfig(
             runtime=runtime,
             attention_launch=attention_launch,
             qkv_launch=HIP_QKV_LAUNCH if qkv is QKVMaterialization.HIP_NATIVE_BHSD else None,
-            residual_norm_launch=norm_launch,
+            residual_norm_launch=residual_launch,
             initial_norm_launch=norm_launch,
             ffn_launch=HIP_GELU_LAUNCH if ffn is FFNBackend.HIP_EXACT_GELU else None,
             ffn_input_launch=HIP_LINEAR_LAUNCH if ffn is FFNBackend.HIP_LINEAR_EXACT_GELU else None,
@@ -740,6 +776,8 @@ __all__ = [
     "HIP_QKV_LAUNCH",
     "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",
     "HIP_RESIDUAL_NORM_BACKENDS",
+    "LINEAR_BOUNDARY_RESIDUAL_NORM_BACKENDS",
+    "hip_linear_boundary_launch",
     "LAUNCHED_ATTENTION_BACKENDS",
     "NATIVE_QKV_MATERIALIZATIONS",
     "TRITON_ATTENTION_BACKENDS",

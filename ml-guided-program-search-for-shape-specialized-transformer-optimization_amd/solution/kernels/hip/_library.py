@@ -76,6 +76,11 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
         _int,
     ),
     "sah_qkv_launch_supported": ([_int] * 4, _int),
+    "sah_linear_residual_norm": (
+        [_ptr] * 8 + [_i64] * 4 + [ctypes.c_float] + [_int] * 4 + [_ptr],
+        _int,
+    ),
+    "sah_linear_residual_norm_launch_supported": ([_i64, _int, _int], _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -26,6 +26,7 @@ from .config import (
     GemmLaunchParams,
     InitialNormBackend,
     LAUNCHED_ATTENTION_BACKENDS,
+    LINEAR_BOUNDARY_RESIDUAL_NORM_BACKENDS,
     NormLaunchParams,
     PrecisionPlan,
     ProjectionBackend,
@@ -218,6 +219,13 @@ class ExecutionPlan:
             ResidualNormBackend.HIP_FUSED,
             ResidualNormBackend.HIP_MIXED,
         }
+
+    @property
+    def use_linear_boundary_fusion(self) -> bool:
+        """The output projections are fused into their residual boundaries
+        (reference :259-260)."""
+
+        return self.residual_norm_backend in LINEAR_BOUNDARY_RESIDUAL_NORM_BACKENDS
 
     @property
     def use_mixed_residual_stream(self) -> bool:

@@ -142,6 +142,7 @@ class HardwareCapabilities:
     hip_linear_exact_gelu: bool = False
     hip_exact_gelu: bool = False
     hip_qkv_native_bhsd: bool = False
+    hip_linear_residual_norm: bool = False
 
     @property
     def is_gfx950(self) -> bool:
@@ -191,6 +192,7 @@ class HardwareCapabilities:
             hip_linear_exact_gelu=hip_available,
             hip_exact_gelu=hip_available,
             hip_qkv_native_bhsd=hip_available,
+            hip_linear_residual_norm=hip_available,
         )
 
 
@@ -560,6 +562,9 @@ class PlanBuilder:
         backend = config.program.residual_norm
         if backend is ResidualNormBackend.TORCH:
             return
+        if backend is ResidualNormBackend.HIP_LINEAR_FUSED:
+            PlanBuilder._validate_linear_boundary(config, context, hardware, reject)
+            return
         if backend not in {ResidualNormBackend.HIP_FUSED, ResidualNormBackend.HIP_MIXED}:
             what = (
                 "torch.compile residual norm"
@@ -599,6 +604,50 @@ class PlanBuilder:
                 "requires_fp16_update",
                 "program.precision_plan",
                 "mixed residual norm requires FP16 attention and FFN updates",
+            )
+
+    @staticmethod
+    def _validate_linear_boundary(
+        config: ConfigSpec,
+        context: ExecutionContext,
+        hardware: HardwareCapabilities,
+        reject: Reject,
+    ) -> None:
+        """The fused Linear + residual + LayerNorm boundary at both residual
+        boundaries of a layer (the reference's TRITON_LINEAR_MIXED rules,
+        solution/plan_builder.py:668-707, 796-801, 950-990), on a 16-bit
+        stream with native-dtype output projections."""
+
+        from .kernels.boundary.hip_linear_residual_norm import launch_config_is_valid, supported_width
+
+        field = "program.residual_norm"
+        _validate_hip_common(context, hardware, hardware.hip_linear_residual_norm, field, reject)
+        if context.dtype not in {torch.float16, torch.bfloat16}:
+            reject("unsupported_dtype", field, "the HIP linear boundary runs on FP16 and BF16 streams")
+        for name in ("attention_output_projection", "ffn_output_projection"):
+            if getattr(config.program, name) is not ProjectionBackend.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    f"program.{name}",
+                    "the HIP linear boundary multiplies the native-dtype projection weights",
+                )
+        if not supported_width(context.d_model, context.d_model) or (
+            context.ffn_dim is None or not supported_width(context.d_model, context.ffn_dim)
+        ):
+            reject(
+                "unsupported_shape",
+                field,
+                "the HIP linear boundary supports d_model 512 and 1024 with ffn_dim % 64 == 0",
+            )
+        if config.schedule.runtime is RuntimeBackend.COMPILED_FORWARD:
+            reject("runtime_incompatible", "schedule.runtime", "the linear boundary is not nested in compiled forward")
+        launch = config.schedule.residual_norm_launch
+        assert launch is not None
+        if not launch_config_is_valid(context.d_model, launch.block_rows, launch.num_warps):
+            reject(
+                "unsupported_launch_value",
+                "schedule.residual_norm_launch",
+                "the HIP linear boundary runs 65536 / d_model rows per workgroup of 8 wavefronts",
             )
 
     # ------------------------------------------------------------- initial norm

@@ -20,6 +20,7 @@ from solution.config import (
     ConfigSpec,
     FFNBackend,
     InitialNormBackend,
+    NormLaunchParams,
     PrecisionPlan,
     ProgramConfig,
     ProjectionBackend,
@@ -63,6 +64,8 @@ def hip_streamed_config(
     microbatch_size: int = DEFAULT_MICROBATCH_SIZE,
     ffn: FFNBackend = FFNBackend.HIP_EXACT_GELU,
     qkv: QKVMaterialization = QKVMaterialization.VIEW,
+    residual_norm: ResidualNormBackend = ResidualNormBackend.HIP_FUSED,
+    boundary_launch: NormLaunchParams | None = None,
 ) -> ConfigSpec:
     """The gfx950 long-sequence program with ordered microbatches."""
 
@@ -71,6 +74,8 @@ def hip_streamed_config(
         attention_launch=HIP_LONG_SEQUENCE_ATTENTION_LAUNCH,
         ffn=ffn,
         qkv=qkv,
+        residual_norm=residual_norm,
+        boundary_launch=boundary_launch,
     )
 
 

@@ -302,7 +302,13 @@ class _SelfAttention(nn.Module):
         causal: bool,
         plan: ExecutionPlan,
         observation: _ExecutionObservation | None,
+        *,
+        project: bool = True,
     ) -> torch.Tensor:
+        """The attention branch.  With ``project=False`` (the linear-boundary
+        plans, reference :620-726) it returns the [B, S, D] context before the
+        output projection, which the fused boundary multiplies."""
+
         batch, seq, _ = value.shape
         backend = plan.attention_backend
         if plan.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD:
@@ -400,7 +406,11 @@ class _SelfAttention(nn.Module):
             raise RuntimeError(
                 f"attention bridge {plan.attention_output_bridge.value} is not executable here"
             )
-        output = self.out_proj.forward_backend(context, plan.attention_output_projection_backend)
+        output = (
+            self.out_proj.forward_backend(context, plan.attention_output_projection_backend)
+            if project
+            else context
+        )
         if observation is not None:
             observation.attention_backends.append(actual_backend)
             observation.attention_compute_dtypes.append(
@@ -415,11 +425,15 @@ class _SelfAttention(nn.Module):
             observation.attention_output_projection_backends.append(
                 plan.attention_output_projection_backend.value
             )
-            observation.attention_output_projection_compute_dtypes.append(_dtype_name(output.dtype))
+            observation.attention_output_projection_compute_dtypes.append(
+                _dtype_name(output.dtype if project else value.dtype)
+            )
             observation.attention_output_projection_launches.append(
                 _launch_dict(plan.attention_output_projection_launch)
             )
             observation.attention_launches.append(_launch_dict(plan.attention_launch))
+        if not project:
+            return output
         if output.dtype != value.dtype and not plan.use_mixed_residual_stream:
             output = output.to(value.dtype)
         if valid_token_mask is not None:
@@ -443,20 +457,26 @@ class _TransformerBlock(nn.Module):
         causal: bool,
         plan: ExecutionPlan,
         observation: _ExecutionObservation | None,
+        *,
+        project: bool = True,
     ) -> torch.Tensor:
-        return self.attention(normalized, valid_token_mask, causal, plan, observation)
+        return self.attention(normalized, valid_token_mask, causal, plan, observation, project=project)
 
     def ffn_update(
         self,
         normalized: torch.Tensor,
         plan: ExecutionPlan,
         observation: _ExecutionObservation | None,
+        *,
+        project: bool = True,
     ) -> torch.Tensor:
         """Exact-GELU FFN (reference :816-1062): the TORCH branch, the
         elementwise Exact-GELU kernel after the input projection (reference
         :945-965, here the gfx950 kernel), or the fused Linear + bias + exact
         GELU input projection (reference :898-935, here the gfx950 kernel);
-        then the output projection."""
+        then the output projection.  With ``project=False`` (the
+        linear-boundary plans, reference :1001-1033) it returns the hidden
+        activation, which the fused boundary multiplies."""
 
         if plan.ffn_backend is FFNBackend.HIP_LINEAR_EXACT_GELU:
             from .kernels.ffn.hip_linear_gelu import (
@@ -504,16 +524,22 @@ class _TransformerBlock(nn.Module):
             if plan.ffn_activation_output_dtype == "float32":
                 projected = projected.float()
             hidden = F.gelu(projected, approximate="none")
-        update = self.ffn_out.forward_backend(hidden, plan.ffn_output_projection_backend)
+        update = (
+            self.ffn_out.forward_backend(hidden, plan.ffn_output_projection_backend) if project else hidden
+        )
         if observation is not None:
             observation.ffn_input_projection_backends.append(plan.ffn_input_projection_backend.value)
             observation.ffn_input_projection_compute_dtypes.append(input_compute_dtype)
             observation.ffn_activation_output_dtypes.append(_dtype_name(hidden.dtype))
             observation.ffn_output_projection_backends.append(plan.ffn_output_projection_backend.value)
-            observation.ffn_output_projection_compute_dtypes.append(_dtype_name(update.dtype))
+            observation.ffn_output_projection_compute_dtypes.append(
+                _dtype_name(update.dtype if project else normalized.dtype)
+            )
             observation.ffn_launches.append(_launch_dict(plan.ffn_launch))
             observation.ffn_input_launches.append(_launch_dict(plan.ffn_input_launch))
             observation.ffn_backends.append(plan.ffn_backend.value)
+        if not project:
+            return update
         if update.dtype != normalized.dtype and not plan.use_mixed_residual_stream:
             update = update.to(normalized.dtype)
         return update
@@ -835,26 +861,39 @@ class UserOptimizedTransformer(nn.Module):
             return self.final_norm(value)
         normalized = self._initial_norm(value, plan, observation)
         causal = bool(self.config.causal)
+        fused = plan.use_linear_boundary_fusion
         for index, layer in enumerate(self.layers):
             if observation is not None:
                 observation.layer_input_dtypes.append(_dtype_name(value.dtype))
-            update = layer.attention_update(normalized, valid_token_mask, causal, plan, observation)
-            value, normalized = self._apply_residual_norm(
-                value, update, layer.norm2, valid_token_mask, plan, observation, final_boundary=False
-            )
             last = index + 1 == len(self.layers)
             next_norm = self.final_norm if last else self.layers[index + 1].norm1
-            update = layer.ffn_update(normalized, plan, observation)
-            value, normalized = self._apply_residual_norm(
-                value,
-                update,
-                next_norm,
-                valid_token_mask,
-                plan,
-                observation,
-                final_boundary=last,
-                out=out if last else None,
-            )
+            if fused:
+                context = layer.attention_update(
+                    normalized, valid_token_mask, causal, plan, observation, project=False
+                )
+                value, normalized = self._apply_linear_boundary(
+                    context, layer.attention.out_proj, value, layer.norm2, plan, observation
+                )
+                hidden = layer.ffn_update(normalized, plan, observation, project=False)
+                value, normalized = self._apply_linear_boundary(
+                    hidden, layer.ffn_out, value, next_norm, plan, observation, out=out if last else None
+                )
+            else:
+                update = layer.attention_update(normalized, valid_token_mask, causal, plan, observation)
+                value, normalized = self._apply_residual_norm(
+                    value, update, layer.norm2, valid_token_mask, plan, observation, final_boundary=False
+                )
+                update = layer.ffn_update(normalized, plan, observation)
+                value, normalized = self._apply_residual_norm(
+                    value,
+                    update,
+                    next_norm,
+                    valid_token_mask,
+                    plan,
+                    observation,
+                    final_boundary=last,
+                    out=out if last else None,
+                )
             if observation is not None:
                 observation.layer_output_dtypes.append(_dtype_name(normalized.dtype))
         if valid_token_mask is not None:
@@ -862,6 +901,55 @@ class UserOptimizedTransformer(nn.Module):
         if observation is not None:
             self._last_execution_observation = observation.describe(len(self.layers))
         return normalized
+
+    @staticmethod
+    def _apply_linear_boundary(
+        source: torch.Tensor,
+        linear: _FP16ShadowLinear,
+        value: torch.Tensor,
+        layer_norm: nn.LayerNorm,
+        plan: ExecutionPlan,
+        observation: _ExecutionObservation | None,
+        *,
+        out: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """A branch's output projection fused with the residual add and the
+        LayerNorm after it (reference: the triton_linear_residual_norm calls,
+        solution/transformer.py:699-725 and :1001-1033, here the gfx950
+        kernel); the update never reaches HBM."""
+
+        from .kernels.boundary.hip_linear_residual_norm import (
+            HIP_LINEAR_RESIDUAL_NORM_BACKEND,
+            hip_linear_residual_norm,
+        )
+
+        if plan.residual_norm_backend is not ResidualNormBackend.HIP_LINEAR_FUSED:
+            raise RuntimeError(f"linear boundary {plan.residual_norm_backend.value} is not executable here")
+        launch = plan.residual_norm_launch
+        if launch is None:
+            raise RuntimeError("HIP linear boundary plan is missing launch parameters")
+        destination = (
+            out if out is not None and out.dtype == value.dtype and out.is_contiguous() else None
+        )
+        value, normalized, marker = hip_linear_residual_norm(
+            source,
+            linear.weight,
+            linear.bias,
+            value,
+            layer_norm,
+            block_rows=launch.block_rows,
+            num_warps=launch.num_warps,
+            out=destination,
+        )
+        actual = _strict_backend_marker(
+            marker,
+            expected_marker=HIP_LINEAR_RESIDUAL_NORM_BACKEND,
+            planned_backend=plan.residual_norm_backend.value,
+        )
+        if observation is not None:
+            observation.residual_norm_backends.append(actual)
+            observation.residual_norm_launches.append(_launch_dict(plan.residual_norm_launch))
+        return value, normalized
 
     @staticmethod
     def _apply_residual_norm(

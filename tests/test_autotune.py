@@ -14,6 +14,7 @@ from autotune.hip_launch_search import (
     WORKLOADS,
     HipLaunchSearch,
     SearchShape,
+    _boundary_variants,
     _ffn_variants,
     _qkv_variants,
     _runtime_variants,
@@ -34,7 +35,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         triton_mixed_residual_norm=False, triton_initial_norm=False, triton_exact_gelu=False,
         triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
         hip_residual_norm=True, hip_initial_norm=True, hip_exact_gelu=True, hip_linear_exact_gelu=True,
-        hip_qkv_native_bhsd=True,
+        hip_qkv_native_bhsd=True, hip_linear_residual_norm=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -165,3 +166,20 @@ def test_qkv_stage_offers_views_and_the_native_layout_kernel():
     # without the kernel the native variant is rejected, never timed
     no_kernel = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_qkv_native_bhsd=False))
     assert no_kernel.legal(variants[0], device) and not no_kernel.legal(variants[1], device)
+
+
+def test_boundary_stage_offers_the_fused_linear_boundary_where_it_exists():
+    from solution.config import ResidualNormBackend, hip_linear_boundary_launch
+
+    device = torch.device("cuda")
+    for workload, legal in (("c2", True), ("c5", True), ("c4", False)):
+        shape = SearchShape(*WORKLOADS[workload])
+        search = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950())
+        base = search.incumbent()
+        variants = _boundary_variants(base, shape.d_model)
+        assert variants[0] == base
+        fused = variants[1]
+        assert fused.program.residual_norm is ResidualNormBackend.HIP_LINEAR_FUSED
+        assert fused.schedule.residual_norm_launch == hip_linear_boundary_launch(shape.d_model)
+        assert fused.schedule.initial_norm_launch == base.schedule.initial_norm_launch
+        assert search.legal(fused, device) is legal, workload  # no 2048-wide instantiation

@@ -161,17 +161,66 @@ def test_native_qkv_plan_matches_the_bf16_reference_path(gpu_device, shape):
     assert observed["qkv_materialization"] == "hip_native_bhsd"
 
 
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (2, 256, 512, 8, 2048, 2),   # BASELINE config 2 widths
+        (1, 300, 1024, 16, 4096, 2),  # long-sequence widths, ragged length
+    ],
+)
+def test_linear_boundary_plan_matches_the_bf16_reference_path(gpu_device, shape):
+    """The program whose output projections are fused into their residual
+    LayerNorm boundaries, end to end against the official bf16 path."""
+
+    from solution.config import ResidualNormBackend, hip_config, hip_linear_boundary_launch
+
+    batch, seq, width, heads, ffn, layers = shape
+    print(f"linear boundary model parity {shape}", flush=True)
+    config = TransformerConfig(batch, seq, width, heads, ffn, layers, True)
+    state = xavier_init_weights(config, seed=1357)
+    x = generate_input(config, seed=1357).to(torch.bfloat16)
+    model = _model(config, state, gpu_device, torch.bfloat16)
+    model.configure_execution(
+        config=hip_config(
+            residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED, boundary_launch=hip_linear_boundary_launch(width)
+        )
+    )
+    model.set_execution_observation(True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    torch.cuda.synchronize()
+    reference = forward(cast_state(state, torch.bfloat16), x, config)
+    exact = forward(cast_state(cast_state(state, torch.bfloat16), torch.float32), x.float(), config)
+    _check_bf16_model(exact, reference.float(), output, f"linear boundary model {shape}")
+    description = model.describe_execution_path()
+    observed = description["observed_execution_signature"]
+    assert observed == description["expected_execution_signature"]
+    assert observed["residual_norm_backend"] == "hip_linear_fused"
+
+
 def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
-    """The graph-replay runtime with both fused GEMM epilogues (native-layout
-    QKV and Linear + exact GELU): several replays with new inputs, eager work
+    """The graph-replay runtime with every fused GEMM epilogue (native-layout
+    QKV, Linear + exact GELU, the Linear + residual + LayerNorm boundaries):
+    several replays with new inputs, eager work
     and synchronizations between them, each bitwise equal to the eager
     program on the same input."""
 
-    from solution.config import FFNBackend, QKVMaterialization, hip_config
+    from solution.config import (
+        FFNBackend,
+        QKVMaterialization,
+        ResidualNormBackend,
+        hip_config,
+        hip_linear_boundary_launch,
+    )
 
     config = TransformerConfig(4, 256, 512, 8, 2048, 2, True)
     state = xavier_init_weights(config, seed=13)
-    options = dict(ffn=FFNBackend.HIP_LINEAR_EXACT_GELU, qkv=QKVMaterialization.HIP_NATIVE_BHSD)
+    options = dict(
+        ffn=FFNBackend.HIP_LINEAR_EXACT_GELU,
+        qkv=QKVMaterialization.HIP_NATIVE_BHSD,
+        residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED,
+        boundary_launch=hip_linear_boundary_launch(512),
+    )
     graph_model = _model(config, state, gpu_device, torch.bfloat16)
     graph_model.configure_execution(config=hip_config(graph=True, **options))
     eager_model = _model(config, state, gpu_device, torch.bfloat16)
@@ -187,19 +236,25 @@ def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
             assert torch.equal(replayed, expected), f"replay {seed} differs from eager"
 
 
-def test_streamed_output_equals_its_chunks_bitwise(gpu_device):
+@pytest.mark.parametrize("boundary", ["hip_fused", "hip_linear_fused"])
+def test_streamed_output_equals_its_chunks_bitwise(gpu_device, boundary):
     """The streamed driver runs ordered chunks and writes each chunk's final
-    norm into the logical output: identical to running the chunks alone."""
+    norm into the logical output: identical to running the chunks alone
+    (with the residual-norm boundaries, or with the fused linear boundary
+    writing the last chunk's output in place)."""
 
-    from solution.config import hip_config
+    from solution.config import ResidualNormBackend, hip_config, hip_linear_boundary_launch
 
+    options = {}
+    if boundary == "hip_linear_fused":
+        options = dict(residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED, boundary_launch=hip_linear_boundary_launch(512))
     config = TransformerConfig(4, 200, 512, 8, 2048, 2, True)
     state = xavier_init_weights(config, seed=7)
     x = generate_input(config, seed=7).to(torch.bfloat16).to(gpu_device)
     streamed = _model(config, state, gpu_device, torch.bfloat16)
-    streamed.configure_execution(config=hip_config(microbatch_size=2))
+    streamed.configure_execution(config=hip_config(microbatch_size=2, **options))
     eager = _model(TransformerConfig(2, 200, 512, 8, 2048, 2, True), state, gpu_device, torch.bfloat16)
-    eager.configure_execution(config=hip_config())
+    eager.configure_execution(config=hip_config(**options))
     with torch.inference_mode():
         whole = streamed(x)
         parts = torch.cat([eager(x[0:2]), eager(x[2:4])])

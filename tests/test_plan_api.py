@@ -57,6 +57,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         hip_linear_exact_gelu=True,
         hip_exact_gelu=True,
         hip_qkv_native_bhsd=True,
+        hip_linear_residual_norm=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -466,3 +467,69 @@ def test_native_qkv_plans_and_rejections():
         native, program=dataclasses.replace(native.program, qkv_materialization=QKVMaterialization.TRITON_NATIVE_BHSD)
     )
     assert ("program.qkv_materialization", "backend_unavailable") in codes(builder.evaluate(triton, _context(), _gfx950()))
+
+
+def test_linear_boundary_plans_and_rejections():
+    """The HIP Linear + residual + LayerNorm boundary: accepted for 16-bit
+    inference on gfx950 at widths 512 and 1024 with its launch, rejected with
+    structured reasons otherwise (the reference's TRITON_LINEAR_MIXED rules,
+    solution/plan_builder.py:668-707)."""
+
+    import dataclasses
+
+    from solution.config import (
+        NormLaunchParams,
+        PrecisionPlan,
+        ProjectionBackend,
+        ResidualNormBackend,
+        RuntimeBackend,
+        hip_linear_boundary_launch,
+    )
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    fused = hip_config(residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED, boundary_launch=hip_linear_boundary_launch(512))
+    assert fused.schedule.residual_norm_launch == NormLaunchParams(128, 8)
+    assert fused.schedule.initial_norm_launch == NormLaunchParams(4, 4)
+    assert ConfigSpec.from_dict(fused.to_dict()) == fused
+    plan = builder.build(fused, _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4), _gfx950())
+    assert plan.use_linear_boundary_fusion and plan.residual_norm_backend is ResidualNormBackend.HIP_LINEAR_FUSED
+    assert plan.expected_trace.to_dict()["residual_norm_calls"] == 8
+    long = hip_streamed_config(
+        residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED, boundary_launch=hip_linear_boundary_launch(1024)
+    )
+    streamed = builder.build(long, _context(), _gfx950())
+    assert streamed.use_streamed_execution and streamed.use_linear_boundary_fusion
+    assert not builder.build(hip_config(), _context(), _gfx950()).use_linear_boundary_fusion
+    with pytest.raises(ValueError, match="boundary_launch"):
+        hip_config(residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED)
+    with pytest.raises(ValueError, match="boundary_launch"):
+        hip_config(boundary_launch=hip_linear_boundary_launch(1024))
+    # the launch must be the width's: 1024-wide rows with the 512 launch
+    wrong = builder.evaluate(fused, _context(), _gfx950())
+    assert ("schedule.residual_norm_launch", "unsupported_launch_value") in codes(wrong)
+    # widths without an instantiation (C4's 2048) are rejected, not replaced
+    wide = hip_config(residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED, boundary_launch=NormLaunchParams(32, 8))
+    rejected = builder.evaluate(wide, _context(batch=16, seq=4096, d=2048, heads=32, ffn=8192), _gfx950())
+    assert ("program.residual_norm", "unsupported_shape") in codes(rejected)
+    unavailable = builder.evaluate(long, _context(), _gfx950(hip_linear_residual_norm=False))
+    assert ("program.residual_norm", "backend_unavailable") in codes(unavailable)
+    fp32 = builder.evaluate(long, _context(dtype=torch.float32), _gfx950())
+    assert ("program.residual_norm", "unsupported_dtype") in codes(fp32)
+    masked = builder.evaluate(long, _context(mask=True), _gfx950())
+    assert ("program.residual_norm", "mask_not_supported") in codes(masked)
+    shadow = dataclasses.replace(
+        long,
+        program=dataclasses.replace(
+            long.program,
+            precision_plan=PrecisionPlan.FP16_FFN_OUTPUT,
+            ffn_output_projection=ProjectionBackend.FP16_SHADOW,
+        ),
+    )
+    assert ("program.ffn_output_projection", "backend_incompatible") in codes(builder.evaluate(shadow, _context(), _gfx950()))
+    compiled = dataclasses.replace(
+        fused,
+        schedule=dataclasses.replace(fused.schedule, runtime=RuntimeBackend.COMPILED_FORWARD, compile_mode="max-autotune"),
+    )
+    c2 = _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4)
+    assert ("schedule.runtime", "runtime_incompatible") in codes(builder.evaluate(compiled, c2, _gfx950()))
