@@ -71,9 +71,10 @@ const char* sah_last_error(void);
  *      kernel then first writes V^T into `workspace`) or seq-contiguous
  *      (v_stride_s == 1, a V^T buffer; no workspace needed).
  * out: [B, S, H*64], element stride 1 on the feature axis.
- * Launch parameters: block_m in {128, 256} query rows per workgroup,
- *      block_n == 64 keys per tile, num_warps == 4 wavefronts (wave64) per
- *      workgroup, num_stages in {1, 2} LDS buffers
+ * Launch parameters: (block_m query rows, num_warps wavefronts) per workgroup
+ *      in {(128, 4), (256, 4), (256, 8), (512, 8)} (32 or 64 query rows per
+ *      wavefront), block_n == 64 keys per tile, num_stages 1 or 2 (LDS
+ *      buffers), or 3 for (128, 4) (the software-pipelined kernel)
  *      (sah_causal_attention_launch_supported() reports the implemented set).
  */
 int sah_causal_attention_bsd(
