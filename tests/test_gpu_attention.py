@@ -92,6 +92,22 @@ def test_baseline_config3_attention(gpu_device, block_m, num_warps, num_stages):
     _assert_parity(reference, output, torch.bfloat16, "config 3")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block_m,num_warps,num_stages", [(128, 4, 3), (256, 8, 2), (512, 8, 2)])
+def test_large_scores_near_one_hot_softmax(gpu_device, dtype, block_m, num_warps, num_stages):
+    """Inputs scaled by 4 (scaled scores with a standard deviation of 16): the
+    softmax of most rows is nearly one-hot, the running maximum rises by large
+    steps and most probabilities underflow to zero.  The online rescaling
+    must still match the fp32 oracle."""
+
+    print(f"large scores {dtype} launch={(block_m, num_warps, num_stages)}", flush=True)
+    q, k, v = _inputs(2, 2, 700, dtype=dtype, seed=99, scale_inputs=4.0)
+    output = _run(q, k, v, gpu_device, block_m=block_m, num_warps=num_warps, num_stages=num_stages)
+    assert bool(torch.isfinite(output).all())
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    _assert_parity(reference, output, dtype, f"large scores {dtype} {block_m}")
+
+
 def test_launch_shapes_and_stages_are_bitwise_identical(gpu_device):
     """Within the double/single-buffered kernel, a query row's result does not
     depend on the tiling of the grid."""
