@@ -455,7 +455,7 @@ def main() -> int:
         print(
             "bench.py measures one GPU only: the long-sequence workload is "
             "data-parallel over independent sequences, so N GPUs would each run "
-            "batch/N sequences with no exchange (see the sharding note in DESIGN.md).",
+            "batch/N sequences with no exchange; this build runs on one GPU.",
             file=sys.stderr,
         )
         return 2
