@@ -198,6 +198,50 @@ def test_linear_boundary_plan_matches_the_bf16_reference_path(gpu_device, shape)
     assert observed["residual_norm_backend"] == "hip_linear_fused"
 
 
+@pytest.mark.parametrize("program", ["default", "all_fused"])
+@pytest.mark.parametrize("shape", [(2, 256, 512, 8, 2048, 2), (1, 300, 1024, 16, 4096, 1)])
+def test_hip_programs_on_an_fp16_model_match_the_fp16_reference_path(gpu_device, shape, program):
+    """Every HIP kernel also takes fp16 operands: the gfx950 program on an
+    fp16 model (the default program, and the one with every fused GEMM
+    epilogue), end to end against the official path run in fp16."""
+
+    from solution.config import (
+        FFNBackend,
+        QKVMaterialization,
+        ResidualNormBackend,
+        hip_config,
+        hip_linear_boundary_launch,
+    )
+
+    batch, seq, width, heads, ffn, layers = shape
+    print(f"fp16 model parity {program} {shape}", flush=True)
+    options = {}
+    if program == "all_fused":
+        options = dict(
+            ffn=FFNBackend.HIP_LINEAR_EXACT_GELU,
+            qkv=QKVMaterialization.HIP_NATIVE_BHSD,
+            residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED,
+            boundary_launch=hip_linear_boundary_launch(width),
+        )
+    config = TransformerConfig(batch, seq, width, heads, ffn, layers, True)
+    state = xavier_init_weights(config, seed=97)
+    x = generate_input(config, seed=97).to(torch.float16)
+    model = _model(config, state, gpu_device, torch.float16)
+    model.configure_execution(config=hip_config(**options))
+    model.set_execution_observation(True)
+    with torch.inference_mode():
+        output = model(x.to(gpu_device))
+    torch.cuda.synchronize()
+    assert output.dtype == torch.float16
+    reference = forward(cast_state(state, torch.float16), x, config)
+    exact = forward(cast_state(cast_state(state, torch.float16), torch.float32), x.float(), config)
+    _check_bf16_model(exact, reference.float(), output, f"fp16 {program} model {shape}")
+    description = model.describe_execution_path()
+    observed = description["observed_execution_signature"]
+    assert observed == description["expected_execution_signature"]
+    assert observed["attention_compute_dtype"] == "float16"
+
+
 def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
     """The graph-replay runtime with every fused GEMM epilogue (native-layout
     QKV, Linear + exact GELU, the Linear + residual + LayerNorm boundaries):
