@@ -109,8 +109,11 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// The 8-wave, 2-stage, 32-rows-per-wave instantiation (the long-sequence
+// launch) must keep 4 wavefronts per SIMD (<= 128 VGPRs): the second bound
+// is the minimum wavefronts per SIMD.
 template <typename T, int QG, int STAGES, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void attn_fwd_kernel(AttnParams p) {
+__global__ __launch_bounds__(WAVES * 64, (QG == 1 && STAGES == 2 && WAVES == 8) ? 4 : 1) void attn_fwd_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
   typedef typename Vec8<T>::pair_type V2;
