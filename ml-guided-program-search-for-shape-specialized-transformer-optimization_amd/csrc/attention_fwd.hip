@@ -31,6 +31,7 @@
 //    (last) query tiles of a head are issued first.
 
 #include <cmath>
+#include <type_traits>
 
 #include "sah_common.hpp"
 
@@ -109,11 +110,17 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// The 8-wave, 2-stage, 32-rows-per-wave instantiation (the long-sequence
-// launch) must keep 4 wavefronts per SIMD (<= 128 VGPRs): the second bound
-// is the minimum wavefronts per SIMD.
+// The 8-wave, 32-rows-per-wave instantiations (the long-sequence launch and
+// its single-buffered twin) must keep 4 wavefronts per SIMD (<= 128 VGPRs):
+// the second bound is the minimum wavefronts per SIMD.  The fp16
+// single-buffered one would spill under it and is left unbounded.
 template <typename T, int QG, int STAGES, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, (QG == 1 && STAGES == 2 && WAVES == 8) ? 4 : 1) void attn_fwd_kernel(AttnParams p) {
+constexpr int attn_min_waves_per_simd() {
+  return (QG == 1 && WAVES == 8 && (STAGES == 2 || std::is_same<T, bf16>::value)) ? 4 : 1;
+}
+
+template <typename T, int QG, int STAGES, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES, WAVES>())) void attn_fwd_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
   typedef typename Vec8<T>::pair_type V2;
