@@ -25,13 +25,19 @@
 //    ds_read_b128.
 //  * The O rescale by exp(m_old - m_new) is skipped when no row of the wave
 //    raised its maximum (then the factor is exactly 1).
-//  * Grid: one workgroup per (batch*head, query tile).  Workgroup ids are
-//    remapped so that consecutive tiles of the same head land on the same XCD
-//    (the hardware deals ids round-robin over the 8 XCDs), and the longest
-//    (last) query tiles of a head are issued first.
+//  * Grid: one workgroup per (batch*head, query tile).  The hardware deals
+//    workgroup ids round-robin over the 8 XCDs; ids are remapped so that all
+//    tiles of a head land on one XCD (its L2 keeps the head's K and V^T) and
+//    each XCD issues its heads in groups: within a group, longest (last)
+//    query tiles first across the group's heads.  The host sizes the groups
+//    to about two rounds of resident workgroups (see head_group_for), which
+//    balances the causal triangle when a head has few query tiles.
 
+#include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "sah_common.hpp"
 
@@ -60,8 +66,40 @@ struct AttnParams {
   int heads;
   int num_q_tiles;
   int num_blocks;
+  int head_group;  // > 0: heads per issue group on one XCD (batch*heads % 8 == 0)
   float c;  // scale * log2(e)
 };
+
+// Workgroup id -> (batch*head, query tile).  With head_group G > 0, XCD x
+// (ids x, x + 8, ...) owns heads x, x + 8, x + 16, ... (k of them) and issues
+// them in groups of G: tile nq-1 of every head of the group, then tile nq-2,
+// and so on (the last group may be smaller).  With G = 0 (batch*heads not a
+// multiple of 8) each XCD takes a contiguous range of head-major ids, longest
+// tile of each head first.  Both are bijections onto the grid.
+__device__ __forceinline__ void tile_of(const AttnParams& p, int& bh, int& q_tile) {
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7;
+  const int local = bid >> 3;
+  const int nq = p.num_q_tiles;
+  if (p.head_group > 0) {
+    const int k = p.num_blocks / (8 * nq);
+    const int span = p.head_group * nq;
+    const int group = local / span;
+    const int r = local - group * span;
+    const int size = min(p.head_group, k - group * p.head_group);
+    const int rank = r / size;
+    bh = xcd + 8 * (group * p.head_group + (r - rank * size));
+    q_tile = nq - 1 - rank;
+  } else {
+    const int nb = p.num_blocks;
+    const int per = nb >> 3;
+    const int rem = nb & 7;
+    const int logical =
+        xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    bh = logical / nq;
+    q_tile = nq - 1 - (logical - bh * nq);
+  }
+}
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -137,17 +175,8 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  // ---- workgroup id -> (batch*head, query tile), XCD-grouped, heavy first.
-  const int bid = blockIdx.x;
-  const int nb = p.num_blocks;
-  const int xcd = bid & 7;
-  const int local = bid >> 3;
-  const int per = nb >> 3;
-  const int rem = nb & 7;
-  const int logical =
-      xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  const int bh = logical / p.num_q_tiles;
-  const int q_tile = p.num_q_tiles - 1 - (logical - bh * p.num_q_tiles);
+  int bh, q_tile;
+  tile_of(p, bh, q_tile);
   const int b = bh / p.heads;
   const int h = bh - b * p.heads;
   const int S = p.seq_len;
@@ -402,16 +431,8 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
-  const int bid = blockIdx.x;
-  const int nb = p.num_blocks;
-  const int xcd = bid & 7;
-  const int local = bid >> 3;
-  const int per = nb >> 3;
-  const int rem = nb & 7;
-  const int logical =
-      xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  const int bh = logical / p.num_q_tiles;
-  const int q_tile = p.num_q_tiles - 1 - (logical - bh * p.num_q_tiles);
+  int bh, q_tile;
+  tile_of(p, bh, q_tile);
   const int b = bh / p.heads;
   const int h = bh - b * p.heads;
   const int S = p.seq_len;
@@ -753,35 +774,72 @@ bool launch_supported(int block_m, int block_n, int num_warps, int num_stages) {
 }
 
 template <typename T, int WAVES>
-void launch_plain(const AttnParams& prm, int qg, int num_stages, hipStream_t stream) {
-  const dim3 grid(prm.num_blocks), block(WAVES * 64);
-  if (qg == 1) {
-    if (num_stages == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 2, WAVES>), grid, block, 0, stream, prm);
-    else
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 1, 1, WAVES>), grid, block, 0, stream, prm);
-  } else {
-    if (num_stages == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 2, WAVES>), grid, block, 0, stream, prm);
-    else
-      hipLaunchKernelGGL((attn_fwd_kernel<T, 2, 1, WAVES>), grid, block, 0, stream, prm);
+const void* plain_kernel(int qg, int num_stages) {
+  if (qg == 1)
+    return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 2, WAVES>)
+                           : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 1, WAVES>);
+  return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 2, WAVES>)
+                         : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 1, WAVES>);
+}
+
+// Workgroups of `kernel` that fit on one CU at once (registers, LDS, waves),
+// cached per kernel; 0 when the runtime cannot say.
+int resident_per_cu(const void* kernel, int threads) {
+  static std::mutex mutex;
+  static std::unordered_map<const void*, int> cache;
+  std::lock_guard<std::mutex> lock(mutex);
+  const auto found = cache.find(kernel);
+  if (found != cache.end()) return found->second;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    blocks = 0;
   }
+  cache.emplace(kernel, blocks);
+  return blocks;
+}
+
+// Heads per issue group (see tile_of).  Each XCD holds slots = CUs/8 x
+// resident workgroups at once; groups of about 2 x slots workgroups let the
+// longest tiles of a group start first while the group stays small enough to
+// keep its heads' K and V^T in the XCD's L2.  Measured on MI355X (bf16):
+// B8 H16 S2048 0.150 -> 0.110 ms (256/64/8/2), B16 H32 S4096 1.74 -> 1.53 ms,
+// B4 H16 S8192 0.82 -> 0.69 ms; long sequences (hundreds of tiles per head)
+// get one head per group, the plain head-major order.  The CU count of the
+// current device is used; the order never changes results.
+int head_group_for(int64_t batch_heads, int64_t q_tiles, const void* kernel, int threads) {
+  if (batch_heads % 8 != 0) return 0;
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int64_t slots = (int64_t)resident_per_cu(kernel, threads) * (cus / 8);
+  if (slots <= 0) return 0;
+  const int64_t heads_per_xcd = batch_heads / 8;
+  const int64_t groups = std::max<int64_t>(1, (heads_per_xcd * q_tiles + slots) / (2 * slots));
+  return (int)ceil_div(heads_per_xcd, groups);
 }
 
 template <typename T>
-int launch_attention(const AttnParams& prm, int block_m, int num_warps, int num_stages,
+int launch_attention(AttnParams prm, int block_m, int num_warps, int num_stages,
                      hipStream_t stream) {
+  const int64_t batch_heads = prm.num_blocks / prm.num_q_tiles;
+  const void* kernel;
+  int threads;
   if (num_stages == 3) {
-    hipLaunchKernelGGL((attn_fwd_pipelined_kernel<T, 1>), dim3(prm.num_blocks), dim3(kThreads), 0,
-                       stream, prm);
+    kernel = reinterpret_cast<const void*>(&attn_fwd_pipelined_kernel<T, 1>);
+    threads = kThreads;
   } else {
     const int qg = block_m / (32 * num_warps);
-    if (num_warps == 8)
-      launch_plain<T, 8>(prm, qg, num_stages, stream);
-    else
-      launch_plain<T, 4>(prm, qg, num_stages, stream);
+    kernel = num_warps == 8 ? plain_kernel<T, 8>(qg, num_stages) : plain_kernel<T, 4>(qg, num_stages);
+    threads = num_warps * 64;
   }
-  return check_hip(hipGetLastError(), "attention kernel launch");
+  prm.head_group = head_group_for(batch_heads, prm.num_q_tiles, kernel, threads);
+  void* args[] = {&prm};
+  return check_hip(hipLaunchKernel(kernel, dim3(prm.num_blocks), dim3(threads), args, 0, stream),
+                   "attention kernel launch");
 }
 
 template <typename T>

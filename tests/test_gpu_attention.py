@@ -177,6 +177,41 @@ def test_first_row_copies_first_value(gpu_device):
         assert torch.equal(output[:, 0, head * 64 : (head + 1) * 64], v[:, head, 0])
 
 
+@pytest.mark.parametrize("block_m,num_warps,num_stages", [(256, 8, 2), (128, 4, 2), (128, 4, 3)])
+@pytest.mark.parametrize("batch,heads,seq", [(5, 16, 8192), (3, 8, 2048), (1, 12, 4096)])
+def test_issue_order_covers_every_tile(gpu_device, block_m, num_warps, num_stages, batch, heads, seq):
+    """Every (batch*head, query tile) workgroup runs exactly once under the
+    grouped issue order, including several head groups with a smaller last
+    one (B5 H16 S8192: 10 heads per XCD) and the fallback order when
+    batch*heads is not a multiple of 8 (B1 H12).
+
+    V is constant per head (a multiple of 1/16, exact in bf16), so every
+    output row of head bh equals that constant: the softmax weights sum to
+    one and the fp32 accumulation error (below 1e-3 relative) is under half
+    a bf16 ulp.  Two calls with different constants make a tile that was
+    never written show the previous call's value."""
+
+    launch = dict(block_m=block_m, num_warps=num_warps, num_stages=num_stages)
+    print(f"issue order launch={launch} shape={(batch, heads, seq)}", flush=True)
+    module = _attention_module()
+    generator = torch.Generator(device=gpu_device).manual_seed(seq + heads)
+    shape = (batch, heads, seq, 64)
+    q, k = (
+        (torch.randn(shape, generator=generator, device=gpu_device) / 8).to(torch.bfloat16)
+        for _ in range(2)
+    )
+    index = torch.arange(batch * heads, device=gpu_device).reshape(batch, heads)
+    for sign in (1.0, -1.0):
+        constants = (sign * ((index % 15) + 1) / 16).to(torch.bfloat16)
+        v = constants[:, :, None, None].expand(shape).contiguous()
+        with torch.inference_mode():
+            output, _ = module.hip_streaming_dh64_causal_attention_bsd(q, k, v, scale=1 / 8, **launch)
+        expected = constants[:, None, :, None].expand(batch, seq, heads, 64).reshape(batch, seq, heads * 64)
+        torch.cuda.synchronize(gpu_device)
+        mismatched = (output != expected).sum().item()
+        assert mismatched == 0, f"{mismatched} elements differ from their head's constant (sign {sign})"
+
+
 @pytest.mark.parametrize("block_m,num_warps,num_stages", LAUNCHES)
 def test_batch_slices_are_independent(gpu_device, block_m, num_warps, num_stages):
     """Running a sub-batch gives bitwise the rows of the full batch (the
