@@ -34,7 +34,9 @@ struct VecIO {
     V v;
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = from_f32<T>(in[i]);
-    *reinterpret_cast<V*>(p) = v;
+    // Streaming store: rows are written once.  Measured on MI355X (bf16,
+    // width 1024): 288 -> 277 us for 200000 rows, 27.4 -> 26.5 us for 16384.
+    __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
   }
 };
 
