@@ -41,6 +41,12 @@ with its projection: the fused HIP Linear + residual + LayerNorm kernel, or
 hipBLASLt F.linear followed by the HIP residual LayerNorm, for the attention
 output projection (D -> D) or the FFN output projection (F -> D).  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
+
+``--kernel attention-c3|norm-c3`` times BASELINE.json's operator-alone
+configuration instead: causal attention at B8 H16 S2048 Dh64 under every
+implemented launch, with V in [B, H, S, 64] and in seq-contiguous layout, or
+the fused residual + LayerNorm on [16384, 1024] under a few launches; each
+line is the mean of ``--repeat`` back-to-back launches.
 """
 
 from __future__ import annotations
@@ -286,6 +292,91 @@ def measured_traffic() -> float | None:
         return None
 
 
+def config3_alone(kind: str, repeat: int) -> int:
+    """causal attention alone at B8 H16 S2048 Dh64 (Q, K,
+    V N(0,1)/sqrt(64); V both [B, H, S, 64] contiguous, which the op stages
+    to V^T, and seq-contiguous)
+    under every implemented launch, or the fused residual + LayerNorm alone
+    on [16384, 1024] bf16 N(0,1) over rotating buffers; prints the mean
+    HIP-event duration of back-to-back launches and its rate."""
+
+    import torch
+
+    from solution.kernels.hip import load_library
+    from solution.kernels.norm import hip_residual
+    from solution.shape14 import hip_streaming_dh64
+
+    load_library()
+    device = torch.device("cuda", 0)
+    generator = torch.Generator(device=device).manual_seed(1234)
+    runs = []
+    with torch.inference_mode():
+        if kind == "attention-c3":
+            q, k, v = (
+                (torch.randn(8, 16, 2048, 64, generator=generator, device=device) / 8).to(torch.bfloat16)
+                for _ in range(3)
+            )
+            flops = _attention_flops(q)
+            # the same V stored seq-contiguous ([B, H, 64, S] transposed view), as
+            # the native QKV projection hands it over: no staging copy
+            v_seq_major = v.transpose(-1, -2).contiguous().transpose(-1, -2)
+            for block_m in (128, 256, 512):
+                for warps in (4, 8):
+                    for stages in (1, 2, 3):
+                        if not hip_streaming_dh64.launch_config_is_valid(block_m, 64, warps, stages):
+                            continue
+                        for layout, value in (("V bhsd", v), ("V seq-major", v_seq_major)):
+                            runs.append((
+                                f"launch ({block_m}, 64, {warps}, {stages}) {layout}",
+                                lambda bm=block_m, w=warps, st=stages, value=value: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
+                                    q, k, value, scale=0.125, block_m=bm, block_n=64, num_warps=w, num_stages=st),
+                                lambda ms: f"{flops / ms / 1e9:.1f} TFLOP/s ({100 * flops / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)",
+                            ))
+        else:
+            # 6 input pairs and the outputs of the last 6 launches kept alive:
+            # every launch touches buffers last used ~0.8 GB earlier, more than
+            # twice the 256 MB Infinity Cache, so the rate is HBM's, not MALL's
+            sets = 6
+            inputs = [
+                (torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16),
+                 torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16))
+                for _ in range(sets)
+            ]
+            outputs = [None] * sets
+            counter = [0]
+            layer_norm = torch.nn.LayerNorm(1024).to(device=device, dtype=torch.bfloat16)
+            nbytes = _norm_bytes(*inputs[0], layer_norm.weight, layer_norm.bias, 1e-5, torch.bfloat16)
+
+            def rotating(block_rows, warps):
+                index = counter[0] % sets
+                counter[0] += 1
+                outputs[index] = None
+                outputs[index] = hip_residual.hip_residual_layer_norm(
+                    *inputs[index], layer_norm, block_rows=block_rows, num_warps=warps)
+
+            for block_rows, warps in ((2, 2), (4, 4), (8, 8), (16, 8)):
+                runs.append((
+                    f"launch ({block_rows} rows, {warps} waves)",
+                    lambda br=block_rows, w=warps: rotating(br, w),
+                    lambda ms: f"{nbytes / ms / 1e6:.1f} GB/s ({100 * nbytes / ms / 1e6 / PEAK_HBM_GBS:.1f}% of 8 TB/s)",
+                ))
+        for label, run, rate in runs:
+            run()  # code loading
+            torch.cuda.synchronize()
+            # back-to-back launches between one event pair: the host enqueues
+            # faster than the GPU drains, so host-side call overhead is hidden
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(repeat):
+                run()
+            end.record()
+            torch.cuda.synchronize()
+            mean = start.elapsed_time(end) / repeat
+            print(f"{kind} {label}: {mean:.4f} ms per launch (mean of {repeat} back-to-back), {rate(mean)}", flush=True)
+    return 0
+
+
 def kernel_alone(kind: str, repeat: int) -> int:
     """Run one kernel alone at the workload's per-chunk shape; print the
     HIP-event duration of every launch."""
@@ -447,7 +538,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
                                              "qkv", "qkv-torch", "boundary", "boundary-torch", "boundary-ffn",
-                                             "boundary-ffn-torch"),
+                                             "boundary-ffn-torch", "attention-c3", "norm-c3"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     args = parser.parse_args()
@@ -461,6 +552,8 @@ def main() -> int:
         return 2
     if args.steps <= 0 or args.warmup < 0:
         raise SystemExit("--steps must be positive and --warmup non-negative")
+    if args.kernel in ("attention-c3", "norm-c3"):
+        return config3_alone(args.kernel, max(1, args.repeat))
     if args.kernel is not None:
         return kernel_alone(args.kernel, max(1, args.repeat))
 
