@@ -42,11 +42,15 @@ hipBLASLt F.linear followed by the HIP residual LayerNorm, for the attention
 output projection (D -> D) or the FFN output projection (F -> D).  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
 
-``--kernel attention-c3|norm-c3`` times BASELINE.json's operator-alone
-configuration instead: causal attention at B8 H16 S2048 Dh64 under every
-implemented launch, with V in [B, H, S, 64] and in seq-contiguous layout, or
-the fused residual + LayerNorm on [16384, 1024] under a few launches; each
-line is the mean of ``--repeat`` back-to-back launches.
+``config3`` in the JSON line reports BASELINE.json's operator-alone
+configuration, timed before the forward on the idle GPU: the attention op
+with the long-sequence launch and the residual LayerNorm with its default
+launch.
+``--kernel attention-c3|norm-c3`` times that configuration alone: causal
+attention at B8 H16 S2048 Dh64 under every implemented launch, with V in
+[B, H, S, 64] and in seq-contiguous layout, or the fused residual +
+LayerNorm on [16384, 1024] under a few launches; each line is the mean of
+``--repeat`` back-to-back launches.
 """
 
 from __future__ import annotations
@@ -292,89 +296,162 @@ def measured_traffic() -> float | None:
         return None
 
 
+def _config3_cases(kind: str, device, *, launches=None):
+    """BASELINE configs[2], the operators alone: causal attention at B8 H16
+    S2048 Dh64 (Q, K, V N(0,1)/sqrt(64), scale 1/8; V both [B, H, S, 64]
+    contiguous, which the op stages to V^T, and seq-contiguous), or the fused
+    residual + LayerNorm on [16384, 1024] bf16 N(0,1) over rotating buffers.
+    Returns (label, run, work) triples: FLOPs or bytes per launch."""
+
+    import torch
+
+    from solution.kernels.norm import hip_residual
+    from solution.shape14 import hip_streaming_dh64
+
+    generator = torch.Generator(device=device).manual_seed(1234)
+    cases = []
+    if kind == "attention-c3":
+        q, k, v = (
+            (torch.randn(8, 16, 2048, 64, generator=generator, device=device) / 8).to(torch.bfloat16)
+            for _ in range(3)
+        )
+        flops = _attention_flops(q)
+        # the same V stored seq-contiguous ([B, H, 64, S] transposed view), as
+        # the native QKV projection hands it over: no staging copy
+        v_seq_major = v.transpose(-1, -2).contiguous().transpose(-1, -2)
+        if launches is None:
+            launches = [
+                (block_m, warps, stages)
+                for block_m in (128, 256, 512)
+                for warps in (4, 8)
+                for stages in (1, 2, 3)
+                if hip_streaming_dh64.launch_config_is_valid(block_m, 64, warps, stages)
+            ]
+        for block_m, warps, stages in launches:
+            for layout, value in (("V bhsd", v), ("V seq-major", v_seq_major)):
+                cases.append((
+                    f"launch ({block_m}, 64, {warps}, {stages}) {layout}",
+                    lambda bm=block_m, w=warps, st=stages, value=value: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
+                        q, k, value, scale=0.125, block_m=bm, block_n=64, num_warps=w, num_stages=st),
+                    flops,
+                ))
+    else:
+        # 6 input pairs and the outputs of the last 6 launches kept alive:
+        # every launch touches buffers last used ~0.8 GB earlier, more than
+        # twice the 256 MB Infinity Cache, so the rate is HBM's, not MALL's
+        sets = 6
+        inputs = [
+            (torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16),
+             torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16))
+            for _ in range(sets)
+        ]
+        outputs = [None] * sets
+        counter = [0]
+        layer_norm = torch.nn.LayerNorm(1024).to(device=device, dtype=torch.bfloat16)
+        nbytes = _norm_bytes(*inputs[0], layer_norm.weight, layer_norm.bias, 1e-5, torch.bfloat16)
+
+        def rotating(block_rows, warps):
+            index = counter[0] % sets
+            counter[0] += 1
+            outputs[index] = None
+            outputs[index] = hip_residual.hip_residual_layer_norm(
+                *inputs[index], layer_norm, block_rows=block_rows, num_warps=warps)
+
+        for block_rows, warps in launches or ((2, 2), (4, 4), (8, 8), (16, 8)):
+            cases.append((
+                f"launch ({block_rows} rows, {warps} waves)",
+                lambda br=block_rows, w=warps: rotating(br, w),
+                nbytes,
+            ))
+    return cases
+
+
+def _back_to_back_ms(run, repeat: int, *, warmup: int = 1, trials: int = 1) -> float:
+    """Mean HIP-event time per launch of `repeat` back-to-back launches (the
+    host enqueues faster than the GPU drains, so host-side call overhead is
+    hidden) after `warmup` untimed launches; the median over `trials`."""
+
+    import torch
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    means = []
+    for _ in range(trials):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeat):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+        means.append(start.elapsed_time(end) / repeat)
+    return sorted(means)[len(means) // 2]
+
+
 def config3_alone(kind: str, repeat: int) -> int:
-    """causal attention alone at B8 H16 S2048 Dh64 (Q, K,
-    V N(0,1)/sqrt(64); V both [B, H, S, 64] contiguous, which the op stages
-    to V^T, and seq-contiguous)
-    under every implemented launch, or the fused residual + LayerNorm alone
-    on [16384, 1024] bf16 N(0,1) over rotating buffers; prints the mean
-    HIP-event duration of back-to-back launches and its rate."""
+    """Time every implemented launch of one operator-alone case and print
+    each mean launch time and its rate."""
 
     import torch
 
     from solution.kernels.hip import load_library
-    from solution.kernels.norm import hip_residual
-    from solution.shape14 import hip_streaming_dh64
 
     load_library()
-    device = torch.device("cuda", 0)
-    generator = torch.Generator(device=device).manual_seed(1234)
-    runs = []
     with torch.inference_mode():
-        if kind == "attention-c3":
-            q, k, v = (
-                (torch.randn(8, 16, 2048, 64, generator=generator, device=device) / 8).to(torch.bfloat16)
-                for _ in range(3)
-            )
-            flops = _attention_flops(q)
-            # the same V stored seq-contiguous ([B, H, 64, S] transposed view), as
-            # the native QKV projection hands it over: no staging copy
-            v_seq_major = v.transpose(-1, -2).contiguous().transpose(-1, -2)
-            for block_m in (128, 256, 512):
-                for warps in (4, 8):
-                    for stages in (1, 2, 3):
-                        if not hip_streaming_dh64.launch_config_is_valid(block_m, 64, warps, stages):
-                            continue
-                        for layout, value in (("V bhsd", v), ("V seq-major", v_seq_major)):
-                            runs.append((
-                                f"launch ({block_m}, 64, {warps}, {stages}) {layout}",
-                                lambda bm=block_m, w=warps, st=stages, value=value: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
-                                    q, k, value, scale=0.125, block_m=bm, block_n=64, num_warps=w, num_stages=st),
-                                lambda ms: f"{flops / ms / 1e9:.1f} TFLOP/s ({100 * flops / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)",
-                            ))
-        else:
-            # 6 input pairs and the outputs of the last 6 launches kept alive:
-            # every launch touches buffers last used ~0.8 GB earlier, more than
-            # twice the 256 MB Infinity Cache, so the rate is HBM's, not MALL's
-            sets = 6
-            inputs = [
-                (torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16),
-                 torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16))
-                for _ in range(sets)
-            ]
-            outputs = [None] * sets
-            counter = [0]
-            layer_norm = torch.nn.LayerNorm(1024).to(device=device, dtype=torch.bfloat16)
-            nbytes = _norm_bytes(*inputs[0], layer_norm.weight, layer_norm.bias, 1e-5, torch.bfloat16)
-
-            def rotating(block_rows, warps):
-                index = counter[0] % sets
-                counter[0] += 1
-                outputs[index] = None
-                outputs[index] = hip_residual.hip_residual_layer_norm(
-                    *inputs[index], layer_norm, block_rows=block_rows, num_warps=warps)
-
-            for block_rows, warps in ((2, 2), (4, 4), (8, 8), (16, 8)):
-                runs.append((
-                    f"launch ({block_rows} rows, {warps} waves)",
-                    lambda br=block_rows, w=warps: rotating(br, w),
-                    lambda ms: f"{nbytes / ms / 1e6:.1f} GB/s ({100 * nbytes / ms / 1e6 / PEAK_HBM_GBS:.1f}% of 8 TB/s)",
-                ))
-        for label, run, rate in runs:
-            run()  # code loading
-            torch.cuda.synchronize()
-            # back-to-back launches between one event pair: the host enqueues
-            # faster than the GPU drains, so host-side call overhead is hidden
-            start = torch.cuda.Event(enable_timing=True)
-            end = torch.cuda.Event(enable_timing=True)
-            start.record()
-            for _ in range(repeat):
-                run()
-            end.record()
-            torch.cuda.synchronize()
-            mean = start.elapsed_time(end) / repeat
-            print(f"{kind} {label}: {mean:.4f} ms per launch (mean of {repeat} back-to-back), {rate(mean)}", flush=True)
+        for label, run, work in _config3_cases(kind, torch.device("cuda", 0)):
+            ms = _back_to_back_ms(run, repeat)
+            if kind == "attention-c3":
+                rate = f"{work / ms / 1e9:.1f} TFLOP/s ({100 * work / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)"
+            else:
+                rate = f"{work / ms / 1e6:.1f} GB/s ({100 * work / ms / 1e6 / PEAK_HBM_GBS:.1f}% of 8 TB/s)"
+            print(f"{kind} {label}: {ms:.4f} ms per launch (mean of {repeat} back-to-back), {rate}", flush=True)
     return 0
+
+
+def config3_summary(repeat: int = 100, warmup: int = 2000, trials: int = 5) -> dict:
+    """The operator-alone figures reported beside the forward: attention with
+    the long-sequence launch (V in the reference's [B, H, S, 64] layout, V^T
+    staging included, and seq-contiguous), the norm with its default launch.
+    Each figure is the median of `trials` means of `repeat` back-to-back
+    launches.  The first case runs `warmup` untimed launches (about 0.2 s)
+    that bring the idle chip to its clock: the first hundreds of launches
+    measured up to 15% slower."""
+
+    import torch
+
+    from solution.config import HIP_LONG_SEQUENCE_ATTENTION_LAUNCH as L
+    from solution.kernels.norm.hip_residual import DEFAULT_BLOCK_ROWS, DEFAULT_NUM_WARPS
+
+    device = torch.device("cuda", 0)
+    with torch.inference_mode():
+        (_, run_bhsd, flops), (_, run_seq, _) = _config3_cases(
+            "attention-c3", device, launches=[(L.block_m, L.num_warps, L.num_stages)])
+        attention_ms = _back_to_back_ms(run_bhsd, repeat, warmup=warmup, trials=trials)
+        attention_seq_ms = _back_to_back_ms(run_seq, repeat, warmup=repeat, trials=trials)
+        del run_bhsd, run_seq
+        ((_, run_norm, nbytes),) = _config3_cases(
+            "norm-c3", device, launches=[(DEFAULT_BLOCK_ROWS, DEFAULT_NUM_WARPS)])
+        norm_ms = _back_to_back_ms(run_norm, repeat, warmup=repeat, trials=trials)
+    tflops = flops / attention_ms / 1e9
+    tflops_seq = flops / attention_seq_ms / 1e9
+    gbs = nbytes / norm_ms / 1e6
+    log(f"config 3: attention {1e3 * attention_ms:.1f} us ({1e3 * attention_seq_ms:.1f} us seq-contiguous V), "
+        f"norm {1e3 * norm_ms:.1f} us")
+    return {
+        "workload": "operators alone (BASELINE configs[2]): attention B8 H16 S2048 Dh64, norm [16384, 1024]",
+        "timing": f"median of {trials} means of {repeat} back-to-back launches, HIP events, "
+                  f"after {warmup} warm-up attention launches, before the forward",
+        "attention_launch": [L.block_m, L.block_n, L.num_warps, L.num_stages],
+        "attention_us": round(1e3 * attention_ms, 2),
+        "attention_tflops": round(tflops, 1),
+        "attention_pct_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "attention_seq_contiguous_v_us": round(1e3 * attention_seq_ms, 2),
+        "attention_seq_contiguous_v_pct_mfma_peak": round(100 * tflops_seq / PEAK_BF16_TFLOPS, 2),
+        "norm_us": round(1e3 * norm_ms, 2),
+        "norm_gbs": round(gbs, 1),
+        "norm_pct_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+    }
 
 
 def kernel_alone(kind: str, repeat: int) -> int:
@@ -557,6 +634,9 @@ def main() -> int:
     if args.kernel is not None:
         return kernel_alone(args.kernel, max(1, args.repeat))
 
+    # The operators alone first: directly after the forward the chip runs hot
+    # and its clock is lower (attention 114 us there against ~102 us here).
+    config3 = config3_summary()
     gpu = gpu_benchmark(args.steps, args.warmup)
     baseline = None if args.no_cpu_baseline else cpu_baseline()
     if baseline is not None:
@@ -613,6 +693,7 @@ def main() -> int:
             "traffic": traffic,
         },
         "cpu_baseline": baseline,
+        "config3": config3,
     }
     print(json.dumps(record), flush=True)
     return 0
