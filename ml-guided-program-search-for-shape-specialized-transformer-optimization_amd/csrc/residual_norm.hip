@@ -43,7 +43,10 @@ struct VecIO {
 
 // TX: residual-stream dtype (value in, residual out); TU: update dtype;
 // TY: normalized dtype; TP: weight/bias dtype.  ITERS * 64 * VEC == width.
-template <typename TX, typename TU, typename TY, typename TP, int ITERS, bool HAS_RES>
+// ONE_ROW: rows_per_wave == 1, compiled as straight-line code, so the affine
+// parameters stay packed until they are used (55 instead of 77 VGPRs at width
+// 1024 bf16: 8 instead of 6 waves per SIMD, 26.6 -> 25.6 us for 16384 rows).
+template <typename TX, typename TU, typename TY, typename TP, int ITERS, bool HAS_RES, bool ONE_ROW>
 __global__ __launch_bounds__(512) void norm_kernel(
     const TX* __restrict__ value, const TU* __restrict__ update,
     const TP* __restrict__ weight, const TP* __restrict__ bias,
@@ -58,26 +61,19 @@ __global__ __launch_bounds__(512) void norm_kernel(
   const int64_t first_row =
       ((int64_t)blockIdx.x * waves + wave) * (int64_t)rows_per_wave;
 
-  // Affine parameters for this lane's columns (L2-resident across rows).
-  float w[N], b[N];
+  // Affine parameters for this lane's columns (L2-resident across rows),
+  // kept in their storage type and widened where they are used.
+  typedef typename VecIO<TP, VEC>::V VP;
+  const bool has_w = weight != nullptr, has_b = bias != nullptr;
+  VP w_raw[ITERS], b_raw[ITERS];
 #pragma unroll
   for (int i = 0; i < ITERS; ++i) {
     const int col = (i * kWave + lane) * VEC;
-    if (weight != nullptr) {
-      VecIO<TP, VEC>::load(weight + col, w + i * VEC);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) w[i * VEC + e] = 1.0f;
-    }
-    if (bias != nullptr) {
-      VecIO<TP, VEC>::load(bias + col, b + i * VEC);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) b[i * VEC + e] = 0.0f;
-    }
+    if (has_w) w_raw[i] = *reinterpret_cast<const VP*>(weight + col);
+    if (has_b) b_raw[i] = *reinterpret_cast<const VP*>(bias + col);
   }
 
-  for (int r = 0; r < rows_per_wave; ++r) {
+  for (int r = 0; r < (ONE_ROW ? 1 : rows_per_wave); ++r) {
     const int64_t row = first_row + r;
     if (row >= rows) return;  // wave-uniform
     const int64_t base = row * (int64_t)WIDTH;
@@ -129,7 +125,11 @@ __global__ __launch_bounds__(512) void norm_kernel(
 
     float y[N];
 #pragma unroll
-    for (int e = 0; e < N; ++e) y[e] = (v[e] - mean) * rstd * w[e] + b[e];
+    for (int e = 0; e < N; ++e) {
+      const float we = has_w ? to_f32(w_raw[e / VEC][e % VEC]) : 1.0f;
+      const float be = has_b ? to_f32(b_raw[e / VEC][e % VEC]) : 0.0f;
+      y[e] = (v[e] - mean) * rstd * we + be;
+    }
 #pragma unroll
     for (int i = 0; i < ITERS; ++i) {
       const int col = (i * kWave + lane) * VEC;
@@ -187,10 +187,16 @@ int launch_typed(const NormArgs& a) {
   TY* normalized = static_cast<TY*>(a.normalized);
 #define SAH_NORM_CASE(IT)                                                        \
   case IT:                                                                       \
-    hipLaunchKernelGGL((norm_kernel<TX, TU, TY, TP, IT, HAS_RES>), dim3(grid),  \
-                       block, 0, a.stream, value, update, weight, bias,          \
-                       residual, normalized, a.rows, a.eps, rows_per_wave,       \
-                       a.norm_kind);                                             \
+    if (rows_per_wave == 1)                                                      \
+      hipLaunchKernelGGL((norm_kernel<TX, TU, TY, TP, IT, HAS_RES, true>),       \
+                         dim3(grid), block, 0, a.stream, value, update, weight,  \
+                         bias, residual, normalized, a.rows, a.eps,              \
+                         rows_per_wave, a.norm_kind);                            \
+    else                                                                         \
+      hipLaunchKernelGGL((norm_kernel<TX, TU, TY, TP, IT, HAS_RES, false>),      \
+                         dim3(grid), block, 0, a.stream, value, update, weight,  \
+                         bias, residual, normalized, a.rows, a.eps,              \
+                         rows_per_wave, a.norm_kind);                            \
     break;
   switch (iters) {
     SAH_NORM_CASE(1)
