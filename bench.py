@@ -613,6 +613,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-config3", action="store_true",
+                        help="skip the operator-alone figures (e.g. for a kernel trace of the forward alone)")
     parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
                                              "qkv", "qkv-torch", "boundary", "boundary-torch", "boundary-ffn",
                                              "boundary-ffn-torch", "attention-c3", "norm-c3"),
@@ -636,7 +638,7 @@ def main() -> int:
 
     # The operators alone first: directly after the forward the chip runs hot
     # and its clock is lower (attention 114 us there against ~102 us here).
-    config3 = config3_summary()
+    config3 = None if args.no_config3 else config3_summary()
     gpu = gpu_benchmark(args.steps, args.warmup)
     baseline = None if args.no_cpu_baseline else cpu_baseline()
     if baseline is not None:
