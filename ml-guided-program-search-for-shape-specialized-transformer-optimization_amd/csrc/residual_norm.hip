@@ -25,8 +25,10 @@ constexpr int kWave = 64;
 template <typename T, int N>
 struct VecIO {
   typedef T V __attribute__((ext_vector_type(N)));
+  // Row data is read once: non-temporal loads (measured 25.5 -> 24.9 us for
+  // 16384 x 1024 bf16 rows, 272 -> 268 us for 200000, outputs bitwise equal).
   static __device__ __forceinline__ void load(const T* p, float* out) {
-    V v = *reinterpret_cast<const V*>(p);
+    V v = __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = to_f32(v[i]);
   }
