@@ -62,6 +62,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 // row; measured 40.50 -> 40.20 ms on the long-sequence chunk and 1.69 ->
 // 1.61 ms at B16 H32 S4096.
 constexpr float kLazyShift = 8.0f;
+// The tile maximum is formed only for rows whose score bound
+// c * |q| * max|k| over the tile exceeds the current shift by more than this
+// many powers of two; every other row's probabilities stay below 2^64, far
+// from fp32 overflow even when summed over 2^31 keys.
+constexpr float kSafeExp = 64.0f;
+// Sequences at least this long get the key-norm pre-pass (one extra read of
+// K).  Measured on MI355X, bf16, pre-pass included: 40.51 -> 38.93 ms on the
+// long-sequence chunk (B2 H16 S100000), 0.645 -> 0.633 ms at B1 H16 S16384,
+// but 1.53 -> 1.57 ms at B16 H32 S4096 and 0.101 -> 0.112 ms at B8 H16 S2048,
+// where the pre-pass costs more than the skipped maxima save.
+constexpr int64_t kKeyNormMinSeq = 16384;
 
 struct AttnParams {
   const void* q;
@@ -78,6 +89,12 @@ struct AttnParams {
   int num_blocks;
   int head_group;  // > 0: heads per issue group on one XCD (batch*heads % 8 == 0)
   float c;  // scale * log2(e)
+  // Largest key norm of every 64-key tile, [batch*heads][key_tiles]
+  // (key_norm_kernel), for the plain kernel's score bound; null when the
+  // host skips that pre-pass (short sequences), and then every tile forms
+  // its row maximum.
+  const float* knorm;
+  int key_tiles;
 };
 
 // Workgroup id -> (batch*head, query tile).  With head_group G > 0, XCD x
@@ -215,6 +232,20 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       qop[g][s] = __builtin_bit_cast(V8, raw);
     }
   }
+  // c * |q| per row: the score bound of a tile is qnc * (its largest |k|).
+  float qnc[QG];
+#pragma unroll
+  for (int g = 0; g < QG; ++g) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (float)qop[g][s][e];
+        ss = fmaf(x, x, ss);
+      }
+    qnc[g] = sqrtf(half_swap_sum(ss)) * p.c;
+  }
 
   // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
   u32x4 k_pref[CPT], v_pref[CPT];
@@ -274,11 +305,16 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   load_tile(0);
   store_tile(0);
   __syncthreads();
+  const bool bounded = p.knorm != nullptr;  // uniform
+  const float* knorm = bounded ? p.knorm + (int64_t)bh * p.key_tiles : nullptr;
+  float kn_next = bounded ? knorm[0] : 0.0f;
 
   for (int j = 0; j < n_tiles; ++j) {
     const int stage = (STAGES == 2) ? (j & 1) : 0;
     const bool has_next = j + 1 < n_tiles;
     if (has_next) load_tile(j + 1);
+    const float kn = kn_next;
+    if (bounded && has_next) kn_next = knorm[j + 1];
     const int k0 = j * kBlockN;
 
     if (k0 <= wq_last) {  // wave-uniform: skip tiles entirely above this wave's rows
@@ -319,17 +355,20 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       V8 pb[QG][4];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
+        // Rows whose bound keeps every probability below 2^kSafeExp skip the
+        // tile maximum.  Rows that need it move their shift up to the tile
+        // maximum only when that exceeds it by more than kLazyShift (log2
+        // units), so the O rescale is rare.  Both decisions are per row, so
+        // results do not depend on the launch.
+        const bool need = !bounded || qnc[g] * kn - m_run[g] * c > kSafeExp;
+        if (__any(need)) {
         float mx = sacc[g][0][0];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
         mx = half_swap_max(mx);
-        // Lazy shift: a row's shift moves up to the tile maximum only when
-        // that exceeds it by more than kLazyShift (log2 units), so the
-        // probabilities stay below 2^kLazyShift and the O rescale is rare.
-        // The decision is per row, so results do not depend on the launch.
-        const bool grow = (mx - m_run[g]) * c > kLazyShift;
+        const bool grow = need && (mx - m_run[g]) * c > kLazyShift;
         if (__any(grow)) {
           const float m_new = grow ? mx : m_run[g];
           const float alpha = exp2f((m_run[g] - m_new) * c);
@@ -339,6 +378,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
           m_run[g] = m_new;
+        }
         }
         const float mc = m_run[g] * c;
         float lsum = l_run[g];
@@ -737,6 +777,36 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   }
 }
 
+// Largest |k| of every 64-key tile of every (batch, head): one wavefront per
+// tile, one key per lane (64 head-dim elements, fp32 sum of squares).
+template <typename T>
+__global__ __launch_bounds__(256) void key_norm_kernel(
+    const T* __restrict__ k, float* __restrict__ out, int64_t k_sb, int64_t k_sh,
+    int64_t k_ss, int heads, int seq_len, int key_tiles, int64_t total_tiles) {
+  const int64_t tile_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile_id >= total_tiles) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int bh = (int)(tile_id / key_tiles);
+  const int tile = (int)(tile_id - (int64_t)bh * key_tiles);
+  const int b = bh / heads;
+  const int h = bh - b * heads;
+  const int key = tile * 64 + lane;
+  float ss = 0.0f;
+  if (key < seq_len) {
+    const T* row = k + b * k_sb + h * k_sh + (int64_t)key * k_ss;
+#pragma unroll
+    for (int c8 = 0; c8 < kHeadDim; c8 += 8) {
+      float f[8];
+      unpack8<T>(load16(row + c8), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+  }
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) ss = fmaxf(ss, __shfl_xor(ss, offset));
+  if (lane == 0) out[tile_id] = sqrtf(ss);
+}
+
 // [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
 // contiguous, zero-filled for keys in [S, S_pad).  One workgroup per 64 keys.
 template <typename T>
@@ -869,6 +939,24 @@ int launch_transpose(const void* v, void* vt, int64_t batch, int64_t heads,
   return check_hip(hipGetLastError(), "V transpose launch");
 }
 
+template <typename T>
+int launch_key_norm(const void* k, float* out, int64_t batch, int64_t heads, int64_t seq_len,
+                    int64_t k_sb, int64_t k_sh, int64_t k_ss, hipStream_t stream) {
+  const int64_t key_tiles = ceil_div(seq_len, 64);
+  const int64_t total = batch * heads * key_tiles;
+  hipLaunchKernelGGL((key_norm_kernel<T>), dim3((unsigned)ceil_div(total, 4)), dim3(256), 0,
+                     stream, static_cast<const T*>(k), out, k_sb, k_sh, k_ss, (int)heads,
+                     (int)seq_len, (int)key_tiles, total);
+  return check_hip(hipGetLastError(), "key norm launch");
+}
+
+// Bytes of the per-tile key-norm table, rounded up to 256; 0 for sequences
+// that run without it.
+size_t key_norm_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
+  if (seq_len < kKeyNormMinSeq) return 0;
+  return (size_t)ceil_div(batch * heads * ceil_div(seq_len, 64) * (int64_t)sizeof(float), 256) * 256;
+}
+
 }  // namespace
 }  // namespace sah
 
@@ -885,10 +973,12 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
                                                        int64_t v_stride_d, int dtype) {
   (void)head_dim;
   (void)v_stride_s;
-  if (v_stride_d != 1) return 0;  // already seq-contiguous (V^T storage)
+  if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  const size_t norms = key_norm_bytes(batch, heads, seq_len);
+  if (v_stride_d != 1) return norms;  // V already seq-contiguous (V^T storage)
   const size_t elem = (dtype == SAH_DTYPE_F32) ? 4 : 2;
-  return (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) *
-         elem;
+  return norms + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) *
+                     elem;
 }
 
 extern "C" int sah_causal_attention_bsd(
@@ -951,26 +1041,43 @@ extern "C" int sah_causal_attention_bsd(
   prm.num_q_tiles = (int)q_tiles;
   prm.num_blocks = (int)blocks;
 
-  int status;
+  // Workspace: the per-tile key-norm table (long sequences), then (reference
+  // V layout only) V^T.
+  const size_t need = sah_causal_attention_workspace_bytes(
+      batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail(SAH_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu", need,
+                workspace_bytes);
+  if (need > 0 && !aligned16(workspace))
+    return fail(SAH_ERR_INVALID_ARGUMENT, "attention workspace must be 16-byte aligned");
+  const size_t norm_bytes = key_norm_bytes(batch, heads, seq_len);
+  void* vt_space = need > 0 ? static_cast<unsigned char*>(workspace) + norm_bytes : nullptr;
+  int status = SAH_OK;
+  prm.knorm = nullptr;
+  prm.key_tiles = (int)ceil_div(seq_len, 64);
+  if (norm_bytes > 0) {
+    float* norms = static_cast<float*>(workspace);
+    status = (dtype == SAH_DTYPE_BF16)
+                 ? launch_key_norm<bf16>(key, norms, batch, heads, seq_len, k_stride_b,
+                                         k_stride_h, k_stride_s, stream)
+                 : launch_key_norm<f16>(key, norms, batch, heads, seq_len, k_stride_b,
+                                        k_stride_h, k_stride_s, stream);
+    if (status != SAH_OK) return status;
+    prm.knorm = norms;
+  }
   if (v_stride_d == 1) {
     // Reference layout: transpose V into the workspace first.
-    const size_t need = sah_causal_attention_workspace_bytes(
-        batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(SAH_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu", need,
-                  workspace_bytes);
-    if (!aligned16(value) || !aligned16(workspace) || v_stride_b % 8 || v_stride_h % 8 ||
-        v_stride_s % 8)
+    if (!aligned16(value) || v_stride_b % 8 || v_stride_h % 8 || v_stride_s % 8)
       return fail(SAH_ERR_INVALID_ARGUMENT,
                   "value must be 16-byte aligned with strides multiple of 8");
     status = (dtype == SAH_DTYPE_BF16)
-                 ? launch_transpose<bf16>(value, workspace, batch, heads, seq_len,
+                 ? launch_transpose<bf16>(value, vt_space, batch, heads, seq_len,
                                           v_stride_b, v_stride_h, v_stride_s, stream)
-                 : launch_transpose<f16>(value, workspace, batch, heads, seq_len,
+                 : launch_transpose<f16>(value, vt_space, batch, heads, seq_len,
                                          v_stride_b, v_stride_h, v_stride_s, stream);
     if (status != SAH_OK) return status;
     const int64_t seq_pad = padded_seq(seq_len);
-    prm.vt = workspace;
+    prm.vt = vt_space;
     prm.v_sb = heads * kHeadDim * seq_pad;
     prm.v_sh = kHeadDim * seq_pad;
     prm.v_sd = seq_pad;

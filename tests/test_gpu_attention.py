@@ -248,6 +248,40 @@ def test_long_sequence_sampled_rows(gpu_device, block_m, num_warps, num_stages):
         _assert_parity(torch.from_numpy(expected).float(), actual, torch.bfloat16, f"head {head}")
 
 
+@pytest.mark.parametrize("case", ["large_scores", "late_outlier_key"])
+def test_score_bound_path_sampled_rows(gpu_device, case):
+    """S = 20000 runs with the key-norm pre-pass, where rows whose score
+    bound c |q| max|k| stays within 2^64 of their shift skip the tile maximum.
+    Large scores (inputs x4) keep the bound above that margin, so every tile
+    forms its maximum; a single late key with a 40x norm makes the bound of
+    its tile jump, and the rows that see it must raise their shift there.
+    Sampled rows against float64 per-row math."""
+
+    seq = 20_000
+    print(f"score-bound attention S={seq} case={case}", flush=True)
+    scale = 4.0 if case == "large_scores" else 1.0
+    q, k, v = _inputs(1, 2, seq, dtype=torch.bfloat16, seed=77, scale_inputs=scale)
+    if case == "late_outlier_key":
+        k[0, :, 15000] = (k[0, :, 15000].float() * 40).to(torch.bfloat16)
+    outputs = [
+        _run(q, k, v, gpu_device, block_m=block_m, num_warps=warps, num_stages=2).float().cpu()
+        for block_m, warps in ((256, 8), (128, 4))
+    ]
+    assert torch.equal(outputs[0], outputs[1])
+    assert bool(torch.isfinite(outputs[0]).all())
+    rng = np.random.default_rng(1)
+    rows = np.unique(np.concatenate([
+        np.arange(0, 20), np.arange(14990, 15030), np.arange(seq - 20, seq), rng.integers(0, seq, 40)
+    ]))
+    for head in range(2):
+        expected = causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(),
+            rows, 1 / 8,
+        )
+        actual = outputs[0][0, rows, head * 64 : (head + 1) * 64]
+        _assert_parity(torch.from_numpy(expected).float(), actual, torch.bfloat16, f"{case} head {head}")
+
+
 def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
     module = _attention_module()
     q, k, v = (t.to(gpu_device) for t in _inputs(1, 1, 64, dtype=torch.bfloat16, seed=1))
