@@ -12,7 +12,9 @@ Printed on stdout: ONE JSON line.  ``value`` is the forward latency in ms
 (lower is better).  ``roofline`` covers the dominant kernel, the causal
 attention: achieved TFLOP/s = algorithmic FLOPs (4*B*H*Dh*S(S+1)/2 per
 launch) / the launches' mean duration, timed with HIP events recorded on the
-launch stream around every attention launch inside the timed region.
+launch stream around every attention call inside the timed region (a call
+also runs the key-norm pre-pass and the V^T staging, about 0.6% of it, so the
+figure is slightly below the attention kernel's own).
 ``cpu_baseline`` times the CPU oracle (fp32 official order, query-blocked
 attention) on a bounded sample of the same workload and scales it to one
 full forward.
