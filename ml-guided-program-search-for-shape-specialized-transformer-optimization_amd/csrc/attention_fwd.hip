@@ -64,9 +64,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyShift = 8.0f;
 // The tile maximum is formed only for rows whose score bound
 // c * |q| * max|k| over the tile exceeds the current shift by more than this
-// many powers of two; every other row's probabilities stay below 2^64, far
-// from fp32 overflow even when summed over 2^31 keys.
-constexpr float kSafeExp = 64.0f;
+// many powers of two.  Every other row's probabilities stay below 2^kSafeExp:
+// for bf16 P (the fp32 exponent range) 2^64, far from overflow even summed
+// over 2^31 keys in fp32; for fp16 P 2^15, below the fp16 maximum of 65504.
+template <typename T>
+constexpr float safe_exponent() {
+  return std::is_same<T, f16>::value ? 15.0f : 64.0f;
+}
 // Sequences at least this long get the key-norm pre-pass (one extra read of
 // K).  Measured on MI355X, bf16, pre-pass included: 40.51 -> 38.93 ms on the
 // long-sequence chunk (B2 H16 S100000), 0.645 -> 0.633 ms at B1 H16 S16384,
@@ -355,12 +359,12 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       V8 pb[QG][4];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
-        // Rows whose bound keeps every probability below 2^kSafeExp skip the
+        // Rows whose bound keeps every probability below 2^safe_exponent skip the
         // tile maximum.  Rows that need it move their shift up to the tile
         // maximum only when that exceeds it by more than kLazyShift (log2
         // units), so the O rescale is rare.  Both decisions are per row, so
         // results do not depend on the launch.
-        const bool need = !bounded || qnc[g] * kn - m_run[g] * c > kSafeExp;
+        const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
         if (__any(need)) {
         float mx = sacc[g][0][0];
 #pragma unroll

@@ -282,6 +282,33 @@ def test_score_bound_path_sampled_rows(gpu_device, case):
         _assert_parity(torch.from_numpy(expected).float(), actual, torch.bfloat16, f"{case} head {head}")
 
 
+def test_fp16_score_bound_keeps_probabilities_in_range(gpu_device):
+    """fp16 P overflows above 65504: on the score-bound path (S >= 16384) an
+    fp16 row may skip its tile maximum only while its bound keeps every
+    probability below 2^15.  Key 15000 is set to 3.8 x query 15005, so that
+    row's score for it is about 40 powers of two above its shift while the
+    tile's bound stays within 2^64 of the shift: bf16 P could skip the
+    maximum there, fp16 P must not (2^40 would be inf)."""
+
+    seq = 20_000
+    print(f"fp16 score-bound attention S={seq}", flush=True)
+    q, k, v = _inputs(1, 2, seq, dtype=torch.float16, seed=5)
+    k[0, :, 15000] = (q[0, :, 15005].float() * 3.8).to(torch.float16)
+    output = _run(q, k, v, gpu_device, block_m=256, num_warps=8, num_stages=2).float().cpu()
+    assert bool(torch.isfinite(output).all())
+    rng = np.random.default_rng(2)
+    rows = np.unique(np.concatenate([
+        np.arange(0, 10), np.arange(14998, 15012), np.arange(seq - 10, seq), rng.integers(0, seq, 40)
+    ]))
+    for head in range(2):
+        expected = causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(),
+            rows, 1 / 8,
+        )
+        actual = output[0, rows, head * 64 : (head + 1) * 64]
+        _assert_parity(torch.from_numpy(expected).float(), actual, torch.float16, f"fp16 head {head}")
+
+
 def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
     module = _attention_module()
     q, k, v = (t.to(gpu_device) for t in _inputs(1, 1, 64, dtype=torch.bfloat16, seed=1))
