@@ -92,7 +92,14 @@ struct AttnParams {
   int num_q_tiles;
   int num_blocks;
   int head_group;  // > 0: heads per issue group on one XCD (batch*heads % 8 == 0)
-  float c;  // scale * log2(e)
+  // c = |scale| * log2(e) > 0 (log2(e) for scale 0).  Every Q dword is loaded
+  // as (raw & q_and) ^ q_xor: the identity for scale > 0, the sign flip of
+  // both 16-bit halves for scale < 0 (so c * (-q).k = scale * log2(e) * q.k),
+  // and zero for scale 0 (every visible key then weighs the same, as in
+  // softmax(0 * s)).  The kernels' running maximum of raw scores relies on
+  // c > 0.
+  float c;
+  uint32_t q_and, q_xor;
   // Largest key norm of every 64-key tile, [batch*heads][key_tiles]
   // (key_norm_kernel), for the plain kernel's score bound; null when the
   // host skips that pre-pass (short sequences), and then every tile forms
@@ -233,6 +240,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     for (int s = 0; s < 4; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
+      raw = (raw & p.q_and) ^ p.q_xor;
       qop[g][s] = __builtin_bit_cast(V8, raw);
     }
   }
@@ -518,6 +526,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
     for (int s = 0; s < 4; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
+      raw = (raw & p.q_and) ^ p.q_xor;
       qop[g][s] = __builtin_bit_cast(V8, raw);
     }
   }
@@ -1038,7 +1047,25 @@ extern "C" int sah_causal_attention_bsd(
   prm.o_ss = o_stride_s;
   prm.seq_len = (int)seq_len;
   prm.heads = (int)heads;
-  prm.c = scale * kLog2e;
+  // The kernels take c = |scale| log2(e) > 0 and fold the sign of the scale
+  // into the query (see AttnParams), so any finite scale is exact: negating a
+  // bf16/fp16 value is exact, and the MFMA sums of negated products are the
+  // negated sums.
+  if (scale > 0.0f) {
+    prm.c = scale * kLog2e;
+    prm.q_and = 0xffffffffu;
+    prm.q_xor = 0u;
+  } else if (scale < 0.0f) {
+    prm.c = -scale * kLog2e;
+    prm.q_and = 0xffffffffu;
+    prm.q_xor = 0x80008000u;
+  } else {
+    prm.c = kLog2e;
+    prm.q_and = 0u;
+    prm.q_xor = 0u;
+  }
+  if (!(prm.c > 0.0f) || !std::isfinite(prm.c))
+    return fail(SAH_ERR_INVALID_ARGUMENT, "scale * log2(e) must be a finite nonzero float");
   const int64_t q_tiles = ceil_div(seq_len, block_m);
   const int64_t blocks = q_tiles * batch * heads;
   if (blocks > INT32_MAX) return fail(SAH_ERR_UNSUPPORTED, "too many attention tiles");
@@ -1059,7 +1086,9 @@ extern "C" int sah_causal_attention_bsd(
   int status = SAH_OK;
   prm.knorm = nullptr;
   prm.key_tiles = (int)ceil_div(seq_len, 64);
-  if (norm_bytes > 0) {
+  // The pipelined kernel (num_stages 3) keeps the exact running maximum and
+  // never reads the table; its region of the workspace then stays unused.
+  if (norm_bytes > 0 && num_stages != 3) {
     float* norms = static_cast<float*>(workspace);
     status = (dtype == SAH_DTYPE_BF16)
                  ? launch_key_norm<bf16>(key, norms, batch, heads, seq_len, k_stride_b,

@@ -90,15 +90,19 @@ class ModelParity:
 
     ``candidate`` and ``reference_path`` (the official op order run in the
     same 16-bit dtype) are both compared with ``exact`` (the same forward in
-    fp32 from the same rounded weights and inputs).  The candidate passes when
-    it is no less accurate than the reference path, up to the run-to-run
-    spread of two 16-bit pipelines: max-abs within 1.25x of the reference
-    path's (or within the 2e-2 gate), mean-abs within 1.25x (+1e-4), and at
-    most 1.25x as many elements outside the elementwise 2e-2 / 1e-2 gate
-    (+1e-4 of the elements).
-    A strict elementwise gate between two 16-bit pipelines is below the noise
-    floor: a one-ulp rounding flip of a residual-stream value of magnitude
-    4-8 is 0.03-0.06 before the final LayerNorm.
+    fp32 from the same rounded weights and inputs).  ``passed`` is the rule of
+    ``autotune.accuracy.summary_no_less_accurate`` (the launch search's
+    publication gate, one function for both): the candidate is no less
+    accurate than the reference path, up to the spread of two 16-bit
+    pipelines (max-abs within 1.25x or within 2e-2, mean-abs within 1.25x
+    +1e-4, at most 1.25x as many elements outside the 2e-2 / 1e-2 gate
+    +1e-4 of the elements, every element finite).
+
+    The elementwise north-star gate (|err| <= 2e-2 or |err| <= 1e-2 |ref|)
+    is reported beside it, against the reference path and against fp32
+    (``strict_*``): between two bf16-stream pipelines it is below the noise
+    floor (a one-ulp rounding flip of a residual-stream value of magnitude 4-8
+    is 0.03-0.06 before the final LayerNorm), so it is printed, not asserted.
     """
 
     candidate: Comparison
@@ -107,21 +111,46 @@ class ModelParity:
 
     @property
     def passed(self) -> bool:
-        c, r = self.candidate, self.reference_path
-        return (
-            c.max_abs_error <= max(BF16_ATOL, 1.25 * r.max_abs_error)
-            and c.mean_abs_error <= 1.25 * r.mean_abs_error + 1e-4
-            and c.failed_elements <= 1.25 * r.failed_elements + 1e-4 * c.total_elements
-        )
+        from autotune.accuracy import summary_no_less_accurate
+
+        return summary_no_less_accurate(_summary(self.candidate), _summary(self.reference_path))
+
+    @property
+    def strict_vs_reference_path(self) -> bool:
+        return self.candidate_vs_reference_path.passed
+
+    @property
+    def strict_vs_fp32(self) -> bool:
+        return self.candidate.passed
 
     def summary(self) -> str:
         c, r, x = self.candidate, self.reference_path, self.candidate_vs_reference_path
+        verdict = "PASS" if self.passed else "FAIL"
+        strict_r = "pass" if x.passed else "fail"
+        strict_f = "pass" if c.passed else "fail"
         return (
-            f"vs fp32: candidate max_abs={c.max_abs_error:.4g} mean_abs={c.mean_abs_error:.3g} "
-            f"gate_failures={c.failed_elements}/{c.total_elements}; reference path max_abs="
-            f"{r.max_abs_error:.4g} mean_abs={r.mean_abs_error:.3g} gate_failures={r.failed_elements}; "
-            f"candidate vs reference path max_abs={x.max_abs_error:.4g} gate_failures={x.failed_elements}"
+            f"model gate {verdict}; vs fp32: candidate max_abs={c.max_abs_error:.4g} "
+            f"mean_abs={c.mean_abs_error:.3g} gate_failures={c.failed_elements}/{c.total_elements}; "
+            f"reference path max_abs={r.max_abs_error:.4g} mean_abs={r.mean_abs_error:.3g} "
+            f"gate_failures={r.failed_elements}; elementwise 2e-2/1e-2 gate: vs reference path "
+            f"{strict_r} (max_abs={x.max_abs_error:.4g}, failures={x.failed_elements}), "
+            f"vs fp32 {strict_f} (failures={c.failed_elements})"
         )
+
+
+def _summary(comparison: Comparison):
+    """The accuracy rule's view of an elementwise comparison at the bf16 gate."""
+
+    from autotune.accuracy import ErrorSummary
+
+    finite = comparison.max_abs_error != float("inf") and comparison.mean_abs_error == comparison.mean_abs_error
+    return ErrorSummary(
+        max_abs=comparison.max_abs_error if finite else float("inf"),
+        mean_abs=comparison.mean_abs_error if finite else float("inf"),
+        outside=comparison.failed_elements,
+        total=comparison.total_elements,
+        finite=finite,
+    )
 
 
 def model_parity(

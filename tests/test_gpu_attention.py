@@ -42,11 +42,11 @@ def _to_bsd(context_bhsd: torch.Tensor) -> torch.Tensor:
     return context_bhsd.transpose(1, 2).reshape(batch, seq, heads * dim)
 
 
-def _run(q, k, v, device, **launch):
+def _run(q, k, v, device, scale=1 / 8, **launch):
     module = _attention_module()
     with torch.inference_mode():
         output, marker = module.hip_streaming_dh64_causal_attention_bsd(
-            q.to(device), k.to(device), v.to(device), scale=1 / 8, **launch
+            q.to(device), k.to(device), v.to(device), scale=scale, **launch
         )
     assert marker == module.HIP_STREAMING_DH64_CAUSAL_ATTENTION_BSD_BACKEND
     torch.cuda.synchronize(device)
@@ -318,3 +318,38 @@ def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
         with pytest.raises(RuntimeError, match="ineligible"):
             module.hip_streaming_dh64_causal_attention_bsd(q.float(), k.float(), v.float())
     assert not module.can_use_hip_streaming_dh64_causal_attention(q, k, v, causal=False)
+
+
+SCALE_LAUNCHES = [(128, 4, 2), (256, 8, 2), (512, 8, 1), (128, 4, 3)]
+
+
+@pytest.mark.parametrize("block_m,num_warps,num_stages", SCALE_LAUNCHES)
+@pytest.mark.parametrize("seq", [300, 16500])
+def test_zero_scale_is_the_prefix_mean(gpu_device, block_m, num_warps, num_stages, seq):
+    """softmax(0 * s + causal mask) weighs every visible key equally: row i is
+    the mean of V[0..i], whatever Q and K hold (the reference scales the
+    scores before its running maximum, so it is defined for any scale).
+    S = 16500 also runs the key-norm score bound."""
+
+    launch = (block_m, num_warps, num_stages)
+    print(f"zero scale launch={launch} seq={seq}", flush=True)
+    q, k, v = _inputs(1, 2, seq, dtype=torch.bfloat16, seed=seq + 3, scale_inputs=3.0)
+    output = _run(q, k, v, gpu_device, scale=0.0, block_m=block_m, num_warps=num_warps, num_stages=num_stages)
+    prefix = v.double().cumsum(dim=2) / torch.arange(1, seq + 1, dtype=torch.float64).view(1, 1, seq, 1)
+    _assert_parity(_to_bsd(prefix.float()), output, torch.bfloat16, f"zero scale {launch}")
+
+
+@pytest.mark.parametrize("block_m,num_warps,num_stages", SCALE_LAUNCHES)
+@pytest.mark.parametrize("scale", [-1 / 8, -0.4])
+def test_negative_scale_matches_oracle_and_negated_query(gpu_device, block_m, num_warps, num_stages, scale):
+    """A negative scale is the oracle's softmax of scale * q.k, and bitwise the
+    positive scale on the negated query."""
+
+    launch = dict(block_m=block_m, num_warps=num_warps, num_stages=num_stages)
+    print(f"negative scale {scale} launch={launch}", flush=True)
+    q, k, v = _inputs(2, 2, 333, dtype=torch.bfloat16, seed=17)
+    output = _run(q, k, v, gpu_device, scale=scale, **launch)
+    assert bool(torch.isfinite(output).all())
+    _assert_parity(_to_bsd(_oracle(q, k, v, scale)), output, torch.bfloat16, f"scale {scale}")
+    flipped = _run(-q, k, v, gpu_device, scale=-scale, **launch)
+    assert torch.equal(output, flipped)

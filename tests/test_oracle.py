@@ -212,3 +212,105 @@ def test_forward_prefix_is_causal(dtype):
     full = forward(state, x, config)
     prefix = forward(state, x[:, :25], TransformerConfig(1, 25, 64, 4, 128, 2, True))
     assert torch.equal(full[:, :25], prefix)
+
+
+# ---------------------------------------------------------------------------
+# The model-level accuracy rule (autotune.accuracy), shared by the launch
+# search's publication gate and oracle.compare.model_parity.
+
+
+def _summary(max_abs=0.1, mean_abs=0.01, outside=100, total=1_000_000, finite=True):
+    from autotune.accuracy import ErrorSummary
+
+    return ErrorSummary(max_abs, mean_abs, outside, total, finite)
+
+
+def test_accuracy_rule_bounds_each_statistic_at_its_own_limit():
+    from autotune.accuracy import summary_no_less_accurate as ok
+
+    incumbent = _summary()
+    assert ok(incumbent, incumbent)
+    # max-abs: within 1.25x of the incumbent's (a wrong factor or a flipped
+    # inequality moves one of these two)
+    assert ok(_summary(max_abs=0.1249), incumbent)
+    assert not ok(_summary(max_abs=0.1251), incumbent)
+    # ... or within the 2e-2 gate when the incumbent is more accurate than that
+    tiny = _summary(max_abs=0.001)
+    assert ok(_summary(max_abs=0.0199), tiny)
+    assert not ok(_summary(max_abs=0.0201), tiny)
+    # mean-abs: 1.25x + 1e-4
+    assert ok(_summary(mean_abs=0.01259), incumbent)
+    assert not ok(_summary(mean_abs=0.01261), incumbent)
+    # elements outside the gate: 1.25x + 1e-4 of the elements (125 + 100)
+    assert ok(_summary(outside=225), incumbent)
+    assert not ok(_summary(outside=226), incumbent)
+    # a non-finite candidate never passes, whatever its statistics
+    assert not ok(_summary(finite=False), incumbent)
+    # the roles are not symmetric: a worse candidate fails against a better incumbent
+    assert ok(_summary(max_abs=0.05, mean_abs=0.005, outside=10), incumbent)
+    assert not ok(incumbent, _summary(max_abs=0.05, mean_abs=0.005, outside=10))
+    with pytest.raises(ValueError):
+        ok(_summary(total=10), incumbent)
+
+
+def test_error_summary_applies_the_or_gate_and_flags_non_finite():
+    from autotune.accuracy import summarize_errors
+
+    reference = torch.tensor([1.0, 5.0, -5.0, 0.0])
+    output = torch.tensor([1.03, 5.03, -5.06, 0.019])
+    s = summarize_errors(output, reference)
+    # 0.03 at |ref| 1 fails both parts; 0.03 at 5 passes the rel part (0.05);
+    # 0.06 at 5 fails both; 0.019 at 0 passes the abs part
+    assert s.outside == 2 and s.total == 4 and s.finite
+    assert s.max_abs == pytest.approx(0.06, abs=1e-6)
+    assert s.mean_abs == pytest.approx((0.03 + 0.03 + 0.06 + 0.019) / 4, abs=1e-6)
+    bad = summarize_errors(torch.tensor([1.0, float("nan"), -5.0, 0.0]), reference)
+    assert not bad.finite and bad.outside == 1 and bad.max_abs == float("inf")
+
+
+def _noisy(exact, scale, seed, dtype=torch.bfloat16):
+    generator = torch.Generator().manual_seed(seed)
+    return (exact + scale * torch.randn(exact.shape, generator=generator)).to(dtype)
+
+
+def test_model_parity_compares_both_pipelines_with_fp32():
+    from oracle.compare import model_parity
+
+    generator = torch.Generator().manual_seed(0)
+    exact = torch.randn(2, 64, 128, generator=generator) * 3
+    reference_path = _noisy(exact, 0.01, 1)
+    # an independent pipeline with the same noise level passes; so does the
+    # reference path itself and a more accurate candidate
+    assert model_parity(exact, reference_path, _noisy(exact, 0.01, 2)).passed
+    assert model_parity(exact, reference_path, reference_path).passed
+    assert model_parity(exact, reference_path, exact.to(torch.bfloat16)).passed
+    # twice the noise, a 1% fraction of far-off elements, a bias or a NaN fail
+    assert not model_parity(exact, reference_path, _noisy(exact, 0.02, 2)).passed
+    far = reference_path.float().clone()
+    far.view(-1)[: far.numel() // 100] += 0.5
+    assert not model_parity(exact, reference_path, far.to(torch.bfloat16)).passed
+    assert not model_parity(exact, reference_path, (exact + 0.05).to(torch.bfloat16)).passed
+    nan = reference_path.float().clone()
+    nan.view(-1)[7] = float("nan")
+    assert not model_parity(exact, reference_path, nan).passed
+    # the candidate is measured against fp32, not against the reference path:
+    # an accurate reference path makes a noisy candidate fail
+    accurate = exact.to(torch.bfloat16)
+    assert not model_parity(exact, accurate, _noisy(exact, 0.01, 2)).passed
+    # the elementwise north-star gate is reported on both sides
+    parity = model_parity(exact, reference_path, _noisy(exact, 0.01, 2))
+    assert parity.strict_vs_reference_path == parity.candidate_vs_reference_path.passed
+    assert "elementwise 2e-2/1e-2 gate" in parity.summary()
+
+
+def test_launch_search_gate_is_the_model_parity_rule():
+    from autotune.accuracy import no_less_accurate
+    from autotune.hip_launch_search import no_less_accurate as search_gate
+    from oracle.compare import model_parity
+
+    assert search_gate is no_less_accurate
+    generator = torch.Generator().manual_seed(3)
+    exact = torch.randn(2, 32, 64, generator=generator) * 2
+    incumbent = _noisy(exact, 0.01, 4)
+    for candidate in (_noisy(exact, 0.01, 5), _noisy(exact, 0.015, 5), _noisy(exact, 0.03, 5)):
+        assert no_less_accurate(candidate, incumbent, exact) == model_parity(exact, incumbent, candidate).passed
