@@ -102,6 +102,36 @@ size_t sah_causal_attention_workspace_bytes(
     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
     int64_t v_stride_s, int64_t v_stride_d, int dtype);
 
+/*
+ * sah_causal_attention_bsd for callers that cannot allocate device memory.
+ *
+ * No counterpart in the reference (its Triton launcher allocates nothing
+ * beyond the output).  It is for callers that may not call hipMalloc: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation.  Arguments are those of sah_causal_attention_bsd without the
+ * workspace pair: the workspace is a static device array of
+ * SAH_ATTENTION_STATIC_WORKSPACE_BYTES (64 MiB) that each GPU holds for the
+ * life of the process.  A call whose sah_causal_attention_workspace_bytes()
+ * exceeds that returns SAH_ERR_WORKSPACE before any launch (for example V in
+ * the reference [B, H, S, 64] layout needs B*H*64*roundup(S, 64)*2 bytes, so
+ * B8 H16 S2048 fits and one 2 x 100000-token chunk does not; a seq-contiguous
+ * V needs only the key-norm table).  All calls on one GPU share its array:
+ * calls that may overlap on that GPU (different streams, or host threads)
+ * race on it and must be serialized by the caller.  Nothing in it needs to
+ * start at zero; every call writes what it reads.
+ */
+#define SAH_ATTENTION_STATIC_WORKSPACE_BYTES (64ull << 20)
+int sah_causal_attention_bsd_static_workspace(
+    const void* query, const void* key, const void* value, void* output,
+    int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s, int64_t v_stride_d,
+    int64_t o_stride_b, int64_t o_stride_s,
+    float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages,
+    sah_stream_t stream);
+
 /* 1 when (block_m, block_n, num_warps, num_stages) is an implemented launch. */
 int sah_causal_attention_launch_supported(int block_m, int block_n, int num_warps,
                                           int num_stages);

@@ -40,7 +40,6 @@
 #include <cmath>
 #include <mutex>
 #include <type_traits>
-#include <unordered_map>
 
 #include "sah_common.hpp"
 
@@ -881,19 +880,29 @@ const void* plain_kernel(int qg, int num_stages) {
 }
 
 // Workgroups of `kernel` that fit on one CU at once (registers, LDS, waves),
-// cached per kernel; 0 when the runtime cannot say.
+// cached per kernel in a fixed table (the library has fewer attention
+// kernels than slots; a kernel past the table is queried every time); 0 when
+// the runtime cannot say.
 int resident_per_cu(const void* kernel, int threads) {
+  struct Slot {
+    const void* kernel;
+    int blocks;
+  };
   static std::mutex mutex;
-  static std::unordered_map<const void*, int> cache;
+  static Slot cache[32] = {};
   std::lock_guard<std::mutex> lock(mutex);
-  const auto found = cache.find(kernel);
-  if (found != cache.end()) return found->second;
+  for (const Slot& slot : cache)
+    if (slot.kernel == kernel) return slot.blocks;
   int blocks = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0) != hipSuccess) {
     (void)hipGetLastError();
     blocks = 0;
   }
-  cache.emplace(kernel, blocks);
+  for (Slot& slot : cache)
+    if (slot.kernel == nullptr) {
+      slot = {kernel, blocks};
+      break;
+    }
   return blocks;
 }
 
@@ -1129,4 +1138,71 @@ extern "C" int sah_causal_attention_bsd(
   return (dtype == SAH_DTYPE_BF16)
              ? launch_attention<bf16>(prm, block_m, num_warps, num_stages, stream)
              : launch_attention<f16>(prm, block_m, num_warps, num_stages, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Variant of sah_causal_attention_bsd for callers that cannot allocate
+// device memory (code under HIP graph capture, tight serving loops): the
+// workspace (key-norm table and V^T staging) lives in this file-scope device
+// array, of which each GPU holds its own copy for the life of the process.
+// Kernel arguments need its device address, which differs per GPU and is
+// looked up once per device with hipGetSymbolAddress; the array's name is
+// only a host-side stand-in and is never passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[SAH_ATTENTION_STATIC_WORKSPACE_BYTES];
+
+namespace sah {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, or null on failure
+// (the status is then in sah_last_error()).
+void* scratch_address() {
+  static std::mutex mutex;
+  static void* address[kMaxDevices] = {};
+  int device = 0;
+  if (check_hip(hipGetDevice(&device), "hipGetDevice") != SAH_OK) return nullptr;
+  if (device < 0 || device >= kMaxDevices) {
+    fail(SAH_ERR_UNSUPPORTED, "device ordinal %d exceeds the static workspace table", device);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mutex);
+  if (address[device] == nullptr) {
+    void* ptr = nullptr;
+    if (check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "static workspace lookup") != SAH_OK)
+      return nullptr;
+    address[device] = ptr;
+  }
+  return address[device];
+}
+
+}  // namespace
+}  // namespace sah
+
+extern "C" int sah_causal_attention_bsd_static_workspace(
+    const void* query, const void* key, const void* value, void* output, int64_t batch,
+    int64_t heads, int64_t seq_len, int64_t head_dim, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages, sah_stream_t stream) {
+  const size_t need = sah_causal_attention_workspace_bytes(batch, heads, seq_len, head_dim,
+                                                           v_stride_s, v_stride_d, dtype);
+  if (need > (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES)
+    return fail(SAH_ERR_WORKSPACE,
+                "attention needs %zu workspace bytes, above the static workspace of %zu bytes; "
+                "use sah_causal_attention_bsd with a caller-provided workspace",
+                need, (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES);
+  void* workspace = nullptr;
+  if (need > 0) {
+    workspace = scratch_address();
+    if (workspace == nullptr) return SAH_ERR_HIP;
+  }
+  return sah_causal_attention_bsd(query, key, value, output, batch, heads, seq_len, head_dim,
+                                  q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h,
+                                  k_stride_s, v_stride_b, v_stride_h, v_stride_s, v_stride_d,
+                                  o_stride_b, o_stride_s, scale, dtype, block_m, block_n,
+                                  num_warps, num_stages, workspace,
+                                  need > 0 ? (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES : 0,
+                                  stream);
 }

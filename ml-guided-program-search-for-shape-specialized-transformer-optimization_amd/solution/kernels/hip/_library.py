@@ -57,6 +57,18 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
         + [_ptr, ctypes.c_size_t, _ptr],
         _int,
     ),
+    "sah_causal_attention_bsd_static_workspace": (
+        [_ptr, _ptr, _ptr, _ptr]
+        + [_i64] * 4
+        + [_i64] * 3
+        + [_i64] * 3
+        + [_i64] * 4
+        + [_i64] * 2
+        + [ctypes.c_float, _int]
+        + [_int] * 4
+        + [_ptr],
+        _int,
+    ),
     "sah_causal_attention_workspace_bytes": ([_i64] * 6 + [_int], ctypes.c_size_t),
     "sah_causal_attention_launch_supported": ([_int] * 4, _int),
     "sah_residual_norm": (
@@ -83,6 +95,9 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
     "sah_linear_residual_norm_launch_supported": ([_i64, _int, _int], _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+# SAH_ATTENTION_STATIC_WORKSPACE_BYTES of the header: the device array behind
+# sah_causal_attention_bsd_static_workspace.
+ATTENTION_STATIC_WORKSPACE_BYTES = 64 << 20
 
 
 class HipLibraryError(RuntimeError):

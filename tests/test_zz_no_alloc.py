@@ -1,0 +1,101 @@
+"""sah_causal_attention_bsd_static_workspace, the attention entry point that
+allocates nothing (its workspace is a static device array), against
+sah_causal_attention_bsd with a caller-provided workspace: the same kernels,
+so the outputs must be bitwise equal.  Each case makes two calls in a row,
+the second on a smaller input, so the second reads the array the first left
+behind.  Both entry points are called through the C ABI (ctypes)."""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "shape_aware_hip.h"
+
+
+def _inputs(batch, heads, seq, dtype, seed, seq_major_v, device):
+    generator = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(batch, heads, seq, 64, generator=generator).to(dtype) for _ in range(3))
+    q, k = q.to(device), k.to(device)
+    if not seq_major_v:
+        return q, k, v.to(device)
+    pad = -(-seq // 8) * 8
+    vt = torch.zeros(batch, heads, 64, pad, dtype=dtype)
+    vt[..., :seq] = v.transpose(-2, -1)
+    # [B, H, S, 64] view with seq stride 1, made on the device buffer
+    return q, k, vt.to(device)[..., :seq].transpose(-2, -1)
+
+
+def _call(library, static, q, k, v, launch, scale, dtype_code, stream):
+    batch, heads, seq, _ = q.shape
+    out = torch.full((batch, seq, heads * 64), float("nan"), dtype=q.dtype, device=q.device)
+    args = [q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), batch, heads, seq, 64,
+            *q.stride()[:3], *k.stride()[:3], *v.stride(), out.stride(0), out.stride(1),
+            scale, dtype_code, *launch]
+    if static:
+        status = library.sah_causal_attention_bsd_static_workspace(*args, stream)
+    else:
+        need = library.sah_causal_attention_workspace_bytes(
+            batch, heads, seq, 64, v.stride(2), v.stride(3), dtype_code)
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        status = library.sah_causal_attention_bsd(*args, workspace.data_ptr() if need else None, need, stream)
+    assert status == 0, library.sah_last_error()
+    return out
+
+
+CASES = [
+    # (dtype, seq-contiguous V, launch, first (B, H, S), second smaller (B, H, S))
+    (torch.bfloat16, False, (256, 64, 8, 2), (2, 16, 2048), (1, 4, 700)),
+    (torch.bfloat16, True, (256, 64, 8, 2), (1, 8, 20000), (1, 2, 16400)),
+    (torch.float16, False, (128, 64, 4, 2), (2, 4, 1500), (1, 3, 129)),
+    (torch.bfloat16, False, (128, 64, 4, 3), (1, 4, 17000), (1, 2, 333)),
+]
+
+
+def test_header_states_the_static_workspace_size():
+    from solution.kernels.hip import _library
+
+    match = re.search(r"#define SAH_ATTENTION_STATIC_WORKSPACE_BYTES \((\d+)ull << (\d+)\)", HEADER.read_text())
+    assert match and int(match.group(1)) << int(match.group(2)) == _library.ATTENTION_STATIC_WORKSPACE_BYTES
+
+
+@pytest.mark.parametrize("dtype,seq_major_v,launch,first,second", CASES)
+def test_static_workspace_matches_caller_workspace(gpu_device, dtype, seq_major_v, launch, first, second):
+    from solution.kernels.hip._library import dtype_code, load_library, stream_handle
+
+    library = load_library()
+    stream = stream_handle(gpu_device)
+    for index, shape in enumerate((first, second)):
+        print(f"static workspace dtype={dtype} seq_major_v={seq_major_v} launch={launch} "
+              f"call={index} shape={shape}", flush=True)
+        q, k, v = _inputs(*shape, dtype, 100 + index, seq_major_v, gpu_device)
+        assert (v.stride(2) == 1) == seq_major_v
+        want = _call(library, False, q, k, v, launch, 0.125, dtype_code(dtype), stream)
+        got = _call(library, True, q, k, v, launch, 0.125, dtype_code(dtype), stream)
+        torch.cuda.synchronize(gpu_device)
+        assert bool(torch.isfinite(got).all())
+        assert torch.equal(got, want), f"call {index} {shape}: outputs differ"
+
+
+def test_requests_beyond_the_static_workspace_are_rejected_before_launch(gpu_device):
+    from solution.kernels.hip._library import load_library, stream_handle
+    from solution.kernels.hip import _library
+
+    library = load_library()
+    batch, heads, seq = 2, 16, 100000  # V^T alone is 410 MB
+    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 64, 1, 2)
+    assert need > _library.ATTENTION_STATIC_WORKSPACE_BYTES
+    # full-size buffers, so that no access could leave them even if a launch happened
+    q = torch.zeros(batch, heads, seq, 64, dtype=torch.bfloat16, device=gpu_device)
+    out = torch.empty(batch, seq, heads * 64, dtype=torch.bfloat16, device=gpu_device)
+    status = library.sah_causal_attention_bsd_static_workspace(
+        q.data_ptr(), q.data_ptr(), q.data_ptr(), out.data_ptr(), batch, heads, seq, 64,
+        *q.stride()[:3], *q.stride()[:3], *q.stride(), out.stride(0), out.stride(1),
+        0.125, 2, 256, 64, 8, 2, stream_handle(gpu_device))
+    assert status == _library.SAH_ERR_WORKSPACE
+    assert b"static workspace" in library.sah_last_error()
