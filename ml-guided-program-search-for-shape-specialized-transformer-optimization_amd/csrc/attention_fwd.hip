@@ -185,13 +185,13 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// The 8-wave, 32-rows-per-wave instantiations (the long-sequence launch and
-// its single-buffered twin) must keep 4 wavefronts per SIMD (<= 128 VGPRs):
-// the second bound is the minimum wavefronts per SIMD.  The fp16
-// single-buffered one would spill under it and is left unbounded.
+// The double-buffered 8-wave, 32-rows-per-wave instantiations (the
+// long-sequence launch) must keep 4 wavefronts per SIMD (<= 128 VGPRs): the
+// second bound is the minimum wavefronts per SIMD.  The single-buffered twins
+// would spill under it and are left unbounded.
 template <typename T, int QG, int STAGES, int WAVES>
 constexpr int attn_min_waves_per_simd() {
-  return (QG == 1 && WAVES == 8 && (STAGES == 2 || std::is_same<T, bf16>::value)) ? 4 : 1;
+  return (QG == 1 && WAVES == 8 && STAGES == 2) ? 4 : 1;
 }
 
 template <typename T, int QG, int STAGES, int WAVES>
@@ -789,6 +789,152 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   }
 }
 
+// fp32 causal attention (the reference's fp32 portable path, e.g. BASELINE's
+// CPU configuration run on the GPU): scores, softmax and PV all in fp32 on
+// the VALU, P kept in fp32 (the input dtype, so the reference's rounding of P
+// is the identity).  One workgroup per (batch*head, 64-query tile); four
+// lanes per query row, each owning 16 of a K/V tile's 64 keys: it forms those
+// 16 scores with full 64-element dot products, shares the tile maximum with
+// its three partners (two xor shuffles), and accumulates P V over its keys
+// into a private 64-wide O row.  The partners' O rows and sums are added once
+// at the end.  K and V tiles (64 x 64 fp32, head_dim-contiguous) are staged
+// through LDS; every lane of a quarter reads the same K/V row (broadcast).
+struct AttnF32Params {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_ss;
+  int seq_len;
+  int heads;
+  float c;  // |scale| log2(e), > 0
+  uint32_t q_and, q_xor;
+};
+
+__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnF32Params p) {
+  constexpr int kRows = 64;
+  __shared__ __attribute__((aligned(16))) float k_lds[kBlockN][kHeadDim + 4];
+  __shared__ __attribute__((aligned(16))) float v_lds[kBlockN][kHeadDim + 4];
+  const int tid = threadIdx.x;
+  const int row = tid >> 2;      // query row within the tile
+  const int quarter = tid & 3;   // keys [16*quarter, 16*quarter + 16) of each tile
+  const int bh = blockIdx.y;
+  const int b = bh / p.heads;
+  const int h = bh - b * p.heads;
+  const int S = p.seq_len;
+  const int qi = blockIdx.x * kRows + row;
+  const float* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)min(qi, S - 1) * p.q_ss;
+  const float* kbase = p.k + b * p.k_sb + h * p.k_sh;
+  const float* vbase = p.v + b * p.v_sb + h * p.v_sh;
+
+  float q[kHeadDim];
+#pragma unroll
+  for (int d = 0; d < kHeadDim; d += 4) {
+    u32x4 raw = load16(qrow + d);
+    raw = (raw & p.q_and) ^ p.q_xor;
+    const f32x4 f = __builtin_bit_cast(f32x4, raw);
+    q[d] = f[0];
+    q[d + 1] = f[1];
+    q[d + 2] = f[2];
+    q[d + 3] = f[3];
+  }
+  float o[kHeadDim];
+#pragma unroll
+  for (int d = 0; d < kHeadDim; ++d) o[d] = 0.0f;
+  float m_run = -INFINITY, l_part = 0.0f;
+  const float c = p.c;
+  const int last_query = min(blockIdx.x * kRows + kRows, S) - 1;
+  const int n_tiles = last_query / kBlockN + 1;
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const int k0 = j * kBlockN;
+    __syncthreads();  // the previous tile is no longer read
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int chunk = tid + 256 * i;  // 1024 float4 chunks per 64 x 64 tile
+      const int key = chunk >> 4;
+      const int c4 = (chunk & 15) * 4;
+      u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
+      if (k0 + key < S) {
+        kraw = load16(kbase + (int64_t)(k0 + key) * p.k_ss + c4);
+        vraw = load16(vbase + (int64_t)(k0 + key) * p.v_ss + c4);
+      }
+      *reinterpret_cast<u32x4*>(&k_lds[key][c4]) = kraw;
+      *reinterpret_cast<u32x4*>(&v_lds[key][c4]) = vraw;
+    }
+    __syncthreads();
+    float sc[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = 16 * quarter + e;
+      float dot = 0.0f;
+#pragma unroll
+      for (int d = 0; d < kHeadDim; d += 4) {
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(&k_lds[key][d]);
+        dot = fmaf(q[d], kv[0], dot);
+        dot = fmaf(q[d + 1], kv[1], dot);
+        dot = fmaf(q[d + 2], kv[2], dot);
+        dot = fmaf(q[d + 3], kv[3], dot);
+      }
+      sc[e] = (k0 + key <= qi) ? dot : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    // Rows past the sequence end (qi >= S) see every key and stay finite.
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * c);
+    m_run = m_new;
+    l_part *= alpha;
+#pragma unroll
+    for (int d = 0; d < kHeadDim; ++d) o[d] *= alpha;
+    const float mc = m_new * c;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e], c, -mc));
+      l_part += pe;
+      const int key = 16 * quarter + e;
+#pragma unroll
+      for (int d = 0; d < kHeadDim; d += 4) {
+        const f32x4 vv = *reinterpret_cast<const f32x4*>(&v_lds[key][d]);
+        o[d] = fmaf(pe, vv[0], o[d]);
+        o[d + 1] = fmaf(pe, vv[1], o[d + 1]);
+        o[d + 2] = fmaf(pe, vv[2], o[d + 2]);
+        o[d + 3] = fmaf(pe, vv[3], o[d + 3]);
+      }
+    }
+  }
+  // The four partners share m_run, so their partial sums add directly.
+  l_part += __shfl_xor(l_part, 1);
+  l_part += __shfl_xor(l_part, 2);
+#pragma unroll
+  for (int d = 0; d < kHeadDim; ++d) {
+    o[d] += __shfl_xor(o[d], 1);
+    o[d] += __shfl_xor(o[d], 2);
+  }
+  if (qi >= S) return;
+  const float inv = 1.0f / l_part;
+  float* orow = p.o + b * p.o_sb + (int64_t)qi * p.o_ss + (int64_t)h * kHeadDim + 16 * quarter;
+#pragma unroll
+  for (int d = 0; d < 16; d += 4) {
+    f32x4 out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // o[16 * quarter + d + e], with a compile-time index per quarter
+      float value = 0.0f;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        if (qq == quarter) value = o[16 * qq + d + e];
+      out[e] = value * inv;
+    }
+    store16(orow + d, __builtin_bit_cast(u32x4, out));
+  }
+}
+
 // Largest |k| of every 64-key tile of every (batch, head): one wavefront per
 // tile, one key per lane (64 head-dim elements, fp32 sum of squares).
 template <typename T>
@@ -996,11 +1142,10 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
   (void)head_dim;
   (void)v_stride_s;
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
+  if (dtype == SAH_DTYPE_F32) return 0;  // the fp32 kernel reads K and V as given
   const size_t norms = key_norm_bytes(batch, heads, seq_len);
   if (v_stride_d != 1) return norms;  // V already seq-contiguous (V^T storage)
-  const size_t elem = (dtype == SAH_DTYPE_F32) ? 4 : 2;
-  return norms + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) *
-                     elem;
+  return norms + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
 }
 
 extern "C" int sah_causal_attention_bsd(
@@ -1016,8 +1161,8 @@ extern "C" int sah_causal_attention_bsd(
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention tensors must be non-null");
   if (head_dim != kHeadDim)
     return fail(SAH_ERR_UNSUPPORTED, "head_dim must be 64 (got %lld)", (long long)head_dim);
-  if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16)
-    return fail(SAH_ERR_UNSUPPORTED, "attention dtype must be bf16 or f16");
+  if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16 && dtype != SAH_DTYPE_F32)
+    return fail(SAH_ERR_UNSUPPORTED, "attention dtype must be bf16, f16 or f32");
   if (!launch_supported(block_m, block_n, num_warps, num_stages))
     return fail(SAH_ERR_UNSUPPORTED,
                 "attention launch (block_m=%d, block_n=%d, num_warps=%d, "
@@ -1031,12 +1176,13 @@ extern "C" int sah_causal_attention_bsd(
   if (!std::isfinite(scale)) return fail(SAH_ERR_INVALID_ARGUMENT, "scale must be finite");
 
   // Q and K: 16-byte rows.
+  const int64_t vec = (dtype == SAH_DTYPE_F32) ? 4 : 8;  // elements per 16 bytes
   const int64_t qk_strides[] = {q_stride_b, q_stride_h, q_stride_s,
                                 k_stride_b, k_stride_h, k_stride_s};
   for (int64_t s : qk_strides)
-    if (s % 8 != 0)
+    if (s % vec != 0)
       return fail(SAH_ERR_INVALID_ARGUMENT,
-                  "query/key strides must be multiples of 8 elements");
+                  "query/key strides must be multiples of 16 bytes");
   if (!aligned16(query) || !aligned16(key) || !aligned16(output))
     return fail(SAH_ERR_INVALID_ARGUMENT, "query/key/output must be 16-byte aligned");
   if (o_stride_b % 4 != 0 || o_stride_s % 4 != 0)
@@ -1075,6 +1221,41 @@ extern "C" int sah_causal_attention_bsd(
   }
   if (!(prm.c > 0.0f) || !std::isfinite(prm.c))
     return fail(SAH_ERR_INVALID_ARGUMENT, "scale * log2(e) must be a finite nonzero float");
+  if (dtype == SAH_DTYPE_F32) {
+    // fp32: one kernel for every launch (the launch was validated above and
+    // does not change results), V read head_dim-contiguous as given.
+    if (v_stride_d != 1)
+      return fail(SAH_ERR_UNSUPPORTED, "fp32 attention needs a head_dim-contiguous value");
+    if (!aligned16(value) || v_stride_b % 4 || v_stride_h % 4 || v_stride_s % 4)
+      return fail(SAH_ERR_INVALID_ARGUMENT,
+                  "value must be 16-byte aligned with strides multiple of 4");
+    if (batch * heads > 65535)
+      return fail(SAH_ERR_UNSUPPORTED, "fp32 attention takes at most 65535 batch*heads");
+    AttnF32Params fp;
+    fp.q = static_cast<const float*>(query);
+    fp.k = static_cast<const float*>(key);
+    fp.v = static_cast<const float*>(value);
+    fp.o = static_cast<float*>(output);
+    fp.q_sb = q_stride_b;
+    fp.q_sh = q_stride_h;
+    fp.q_ss = q_stride_s;
+    fp.k_sb = k_stride_b;
+    fp.k_sh = k_stride_h;
+    fp.k_ss = k_stride_s;
+    fp.v_sb = v_stride_b;
+    fp.v_sh = v_stride_h;
+    fp.v_ss = v_stride_s;
+    fp.o_sb = o_stride_b;
+    fp.o_ss = o_stride_s;
+    fp.seq_len = (int)seq_len;
+    fp.heads = (int)heads;
+    fp.c = prm.c;
+    fp.q_and = prm.q_and;
+    fp.q_xor = prm.q_xor != 0u ? 0x80000000u : 0u;
+    hipLaunchKernelGGL(attn_fwd_f32_kernel, dim3((unsigned)ceil_div(seq_len, 64), (unsigned)(batch * heads)),
+                       dim3(256), 0, stream, fp);
+    return check_hip(hipGetLastError(), "fp32 attention launch");
+  }
   const int64_t q_tiles = ceil_div(seq_len, block_m);
   const int64_t blocks = q_tiles * batch * heads;
   if (blocks > INT32_MAX) return fail(SAH_ERR_UNSUPPORTED, "too many attention tiles");

@@ -33,7 +33,7 @@ from ..kernels.hip._library import (
 
 HIP_STREAMING_DH64_CAUSAL_ATTENTION_BSD_BACKEND = "hip_streaming_dh64_causal_attention_bsd"
 _HEAD_DIM = 64
-_SUPPORTED_DTYPES = frozenset({torch.bfloat16, torch.float16})
+_SUPPORTED_DTYPES = frozenset({torch.bfloat16, torch.float16, torch.float32})
 _DEFAULT_BLOCK_M = 128
 _DEFAULT_BLOCK_N = 64
 _DEFAULT_NUM_WARPS = 4
@@ -233,10 +233,13 @@ def can_use_hip_streaming_dh64_causal_attention(
         return False
     if not _value_layout_is_supported(value):
         return False
+    if query.dtype == torch.float32 and value.stride(-1) != 1:
+        return False  # the fp32 kernel reads V head_dim-contiguous
+    per_16_bytes = 16 // query.element_size()
     for tensor in (query, key, value):
         if tensor.data_ptr() % 16:
             return False
-        if any(stride % 8 for stride in _strides(tensor) if stride != 1):
+        if any(stride % per_16_bytes for stride in _strides(tensor) if stride != 1):
             return False
     if not hip_streaming_dh64_causal_attention_available():
         return False

@@ -91,11 +91,11 @@ def validate_hip_streaming_attention(
             "program.attention",
             "HIP streaming attention is specialized for head_dim 64",
         )
-    if qkv_dtype not in {"bfloat16", "float16"}:
+    if qkv_dtype not in {"bfloat16", "float16", "float32"}:
         reject(
-            "requires_16bit_qkv",
+            "unsupported_dtype",
             "program.qkv_projection",
-            "HIP streaming attention requires BF16 or FP16 QKV",
+            "HIP streaming attention supports BF16, FP16 and FP32 QKV",
         )
     launch = config.schedule.attention_launch
     if launch is None:

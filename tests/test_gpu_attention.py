@@ -315,8 +315,13 @@ def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
     with torch.inference_mode():
         with pytest.raises(ValueError):
             module.prevalidated_hip_streaming_dh64_causal_attention_bsd(q, k, v, block_m=64)
+        # mixed dtypes, and fp32 with a seq-contiguous V (the fp32 kernel reads
+        # V head_dim-contiguous), are ineligible
         with pytest.raises(RuntimeError, match="ineligible"):
-            module.hip_streaming_dh64_causal_attention_bsd(q.float(), k.float(), v.float())
+            module.hip_streaming_dh64_causal_attention_bsd(q.float(), k, v)
+        vt = v.float().transpose(-2, -1).contiguous().transpose(-2, -1)
+        with pytest.raises(RuntimeError, match="ineligible"):
+            module.hip_streaming_dh64_causal_attention_bsd(q.float(), k.float(), vt)
     assert not module.can_use_hip_streaming_dh64_causal_attention(q, k, v, causal=False)
 
 
@@ -353,3 +358,42 @@ def test_negative_scale_matches_oracle_and_negated_query(gpu_device, block_m, nu
     _assert_parity(_to_bsd(_oracle(q, k, v, scale)), output, torch.bfloat16, f"scale {scale}")
     flipped = _run(-q, k, v, gpu_device, scale=-scale, **launch)
     assert torch.equal(output, flipped)
+
+
+@pytest.mark.parametrize("block_m,num_warps,num_stages", [(128, 4, 2), (256, 8, 2)])
+@pytest.mark.parametrize(
+    "batch,heads,seq",
+    [(1, 1, 1), (1, 2, 17), (2, 3, 100), (2, 2, 257), (1, 2, 1000), (3, 1, 130), (2, 4, 128)],
+)
+def test_fp32_attention_matches_oracle_at_1e4(gpu_device, block_m, num_warps, num_stages, batch, heads, seq):
+    """fp32 inputs: the fp32 kernel (scores, softmax and PV in fp32, P not
+    rounded) against the oracle's fp32 query-block order, at the fp32 gate
+    |err| <= 1e-4 or |err| <= 1e-4 |ref|."""
+
+    print(f"fp32 attention launch={(block_m, num_warps, num_stages)} shape={(batch, heads, seq)}", flush=True)
+    q, k, v = _inputs(batch, heads, seq, dtype=torch.float32, seed=seq * 5 + heads)
+    output = _run(q, k, v, gpu_device, block_m=block_m, num_warps=num_warps, num_stages=num_stages)
+    assert output.dtype == torch.float32
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    _assert_parity(reference, output, torch.float32, f"fp32 {(batch, heads, seq)}")
+
+
+@pytest.mark.parametrize("scale", [0.0, -0.125])
+def test_fp32_attention_scale_sign_and_packed_views(gpu_device, scale):
+    """fp32 through packed-QKV views (row stride 3D), with a zero and a
+    negative scale."""
+
+    batch, heads, seq = 2, 4, 300
+    generator = torch.Generator().manual_seed(11)
+    packed = torch.randn(batch, seq, 3 * heads * 64, generator=generator)
+    q, k, v = (packed[..., i * heads * 64 : (i + 1) * heads * 64].view(batch, seq, heads, 64).transpose(1, 2)
+               for i in range(3))
+    module = _attention_module()
+    device_packed = packed.to(gpu_device)
+    dq, dk, dv = (device_packed[..., i * heads * 64 : (i + 1) * heads * 64].view(batch, seq, heads, 64).transpose(1, 2)
+                  for i in range(3))
+    with torch.inference_mode():
+        output, _ = module.hip_streaming_dh64_causal_attention_bsd(dq, dk, dv, scale=scale)
+    torch.cuda.synchronize(gpu_device)
+    reference = _to_bsd(_oracle(q, k, v, scale))
+    _assert_parity(reference, output, torch.float32, f"fp32 packed scale {scale}")

@@ -67,6 +67,8 @@ def test_host_only_entry_points():
     # Shorter sequences need only the V^T buffer, and seq-contiguous V none.
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 64, 1, 2) == 8 * 16 * 64 * 2048 * 2
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 1, 2048, 2) == 0
+    # fp32 reads K and V as given: no table, no V^T
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 64, 1, 0) == 0
 
 
 def test_invalid_arguments_fail_before_launch():

@@ -14,6 +14,7 @@ from solution.config import (
     AttentionBackend,
     AttentionLaunchParams,
     ConfigSpec,
+    FFNBackend,
     InitialNormBackend,
     NormLaunchParams,
     ProgramConfig,
@@ -186,8 +187,13 @@ def test_hip_plan_rejections_are_structured():
     assert ("program.attention", "requires_gfx950") in codes(mi300)
     wide_heads = builder.evaluate(hip_config(), _context(heads=8), _gfx950())
     assert ("program.attention", "unsupported_shape") in codes(wide_heads)
-    fp32 = builder.evaluate(hip_config(), _context(dtype=torch.float32), _gfx950())
-    assert ("program.qkv_projection", "requires_16bit_qkv") in codes(fp32)
+    # fp32 models: HIP attention (the fp32 kernel) and HIP norms, torch's FFN
+    # activation; the 16-bit elementwise GELU kernel rejects the fp32 context
+    fp32 = builder.evaluate(hip_config(ffn=FFNBackend.TORCH), _context(dtype=torch.float32), _gfx950())
+    assert not fp32.violations, fp32.violations
+    fp32_gelu = builder.evaluate(hip_config(), _context(dtype=torch.float32), _gfx950())
+    assert ("program.ffn", "unsupported_dtype") in codes(fp32_gelu)
+    assert not any(field == "program.qkv_projection" for field, _ in codes(fp32_gelu))
     missing = builder.evaluate(hip_config(), _context(), _gfx950(hip_streaming_dh64_attention=False,
                                                                   hip_residual_norm=False))
     assert ("program.attention", "backend_unavailable") in codes(missing)
