@@ -230,7 +230,9 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   const int key_end = min(q0 + BM, S);
   const int n_tiles = (key_end + kBlockN - 1) / kBlockN;
 
-  // ---- Q^T operands (B operand of S^T = K Q^T), kept in registers.
+  // ---- Q^T operands (B operand of S^T = K Q^T), kept in registers; the
+  // sign fold of a non-positive scale is skipped (uniform branch) otherwise.
+  const bool q_transform = p.q_and != 0xffffffffu || p.q_xor != 0u;
   V8 qop[QG][4];
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     for (int s = 0; s < 4; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
-      raw = (raw & p.q_and) ^ p.q_xor;
+      if (q_transform) raw = (raw & p.q_and) ^ p.q_xor;
       qop[g][s] = __builtin_bit_cast(V8, raw);
     }
   }
@@ -317,7 +319,12 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   store_tile(0);
   __syncthreads();
   const bool bounded = p.knorm != nullptr;  // uniform
-  const float* knorm = bounded ? p.knorm + (int64_t)bh * p.key_tiles : nullptr;
+  // Global address space spelled out: the table entry of the next tile is
+  // then a scalar load (uniform address, read-only).  Left to inference the
+  // compiler emitted a flat load here, whose completion every later LDS wait
+  // of the loop also waited for (6% slower on the long-sequence chunk).
+  typedef const __attribute__((address_space(1))) float* GlobalFloats;
+  GlobalFloats knorm = bounded ? (GlobalFloats)p.knorm + (int64_t)bh * p.key_tiles : nullptr;
   float kn_next = bounded ? knorm[0] : 0.0f;
 
   for (int j = 0; j < n_tiles; ++j) {
@@ -517,6 +524,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   const int w_tiles = wq_last < 0 ? 0 : wq_last / kBlockN + 1;
   const int j_mask = wq0 / kBlockN;
 
+  const bool q_transform = p.q_and != 0xffffffffu || p.q_xor != 0u;
   V8 qop[QG][4];
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
     for (int s = 0; s < 4; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (qi < S) raw = load16(qbase + (int64_t)qi * p.q_ss + 16 * s + 8 * half);
-      raw = (raw & p.q_and) ^ p.q_xor;
+      if (q_transform) raw = (raw & p.q_and) ^ p.q_xor;
       qop[g][s] = __builtin_bit_cast(V8, raw);
     }
   }
