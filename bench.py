@@ -16,8 +16,19 @@ launch stream around every attention call inside the timed region (a call
 also runs the key-norm pre-pass and the V^T staging, about 0.6% of it, so the
 figure is slightly below the attention kernel's own).
 ``cpu_baseline`` times the CPU oracle (fp32 official order, query-blocked
-attention) on a bounded sample of the same workload and scales it to one
-full forward.
+attention, as the reference's portable path) on the box's host cores: one
+layer of one sequence at the real length S=100000, row-wise work in full and
+the attention on query blocks spread over the sequence (every block scores
+all keys, so all blocks cost the same); ``value`` scales that measured layer
+to the B=32 two-layer forward, an extrapolation labelled as such.
+``cpu_configs`` times the CPU oracle on BASELINE's other configurations
+(C1, C2 whole; C3's operators; one C4 layer).
+
+``semantic_check`` compares, in the same run, one sequence of the timed
+weights through the HIP program with the product's portable program on the
+GPU (bf16 and fp32), as the reference does before timing its long-sequence
+shape.  ``resident_gpu`` times C2 and C4 with their registry programs under
+the reference's formal protocol (20 warm-up calls, 3 x 100 timed calls).
 
 ``roofline.traffic`` is the attention kernel's HBM bytes per launch measured
 by rocprofv3 PMC counters (FETCH_SIZE and WRITE_SIZE, each scaled by what
@@ -173,7 +184,7 @@ def _norm_bytes(value, update, weight, bias, eps, normalized_dtype, *args, **kwa
     return float(rows * width * per + params)
 
 
-def gpu_benchmark(steps: int, warmup: int) -> dict:
+def gpu_benchmark(steps: int, warmup: int, *, check: bool = True) -> dict:
     import torch
 
     from solution.kernels.hip import load_library
@@ -235,7 +246,10 @@ def gpu_benchmark(steps: int, warmup: int) -> dict:
         norm_timer.active = False
         total_ms = start.elapsed_time(end)
     ms_per_step = total_ms / steps
-    assert torch.isfinite(output[:, :: 997]).all(), "non-finite output"
+    if not bool(torch.isfinite(output).all()):
+        raise RuntimeError("the timed forward produced non-finite values")
+    del output
+    semantic = semantic_check(model, x) if check else None
 
     durations, flops = attention_timer.summary()
     attention_ms = sum(durations) / len(durations)
@@ -262,6 +276,7 @@ def gpu_benchmark(steps: int, warmup: int) -> dict:
         "peak_hbm_bytes_per_chunk": int(peak_chunk),
         "model_flops": model_flops,
         "config_id": program.config_id,
+        "semantic_check": semantic,
     }
 
 
@@ -560,53 +575,319 @@ def kernel_alone(kind: str, repeat: int) -> int:
     return 0
 
 
-def cpu_baseline() -> dict:
-    """Time the CPU oracle on a bounded sample and scale to one full forward.
+def _cpu_cores() -> tuple[int, int, float | None]:
+    """(threads used, CPUs in this process's affinity set, cgroup CPU quota):
+    every CPU of the affinity set, unless the cgroup's quota allows fewer."""
 
-    The oracle's fp32 official-order forward (oracle.forward, query-blocked
-    attention: every 128-row block scores all keys, as the reference's
-    portable path does) runs one layer of one sequence of the workload's
-    widths at three lengths S_i.  A least-squares fit t(S) = a*S + b*S^2
-    (row-wise work is linear in S, query-blocked attention quadratic)
-    extrapolates to S = 100000, then x layers x sequences.
-    """
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        limit, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if limit != "max":
+            quota = int(limit) / int(period)
+    except (OSError, ValueError):
+        quota = None
+    threads = affinity if quota is None else max(1, min(affinity, math.floor(quota)))
+    return threads, affinity, quota
 
-    import numpy as np
+
+def _cpu_samples(run, *, warmup: int, samples: int) -> list[float]:
+    """Wall-clock seconds of `samples` calls after `warmup` untimed ones, with
+    time.perf_counter_ns (the official CPU method,
+    official/torch_transformer_benchmark.py:501-506)."""
+
+    for _ in range(warmup):
+        run()
+    times = []
+    for _ in range(samples):
+        start = time.perf_counter_ns()
+        run()
+        times.append((time.perf_counter_ns() - start) / 1e9)
+    return times
+
+
+def _median(values):
+    ordered = sorted(values)
+    middle = len(ordered) // 2
+    return ordered[middle] if len(ordered) % 2 else 0.5 * (ordered[middle - 1] + ordered[middle])
+
+
+def cpu_long_sequence(threads: int, *, blocks_timed: int = 24, full_layer: bool = False) -> dict:
+    """The CPU oracle on one layer of one sequence at the real length
+    S = 100000 (fp32, official op order, the reference portable path's
+    query-blocked attention: every 128-row block scores all S keys, so every
+    block does the same work wherever it sits).
+
+    Measured: the row-wise work of the layer in full (norm1 and the q, k, v
+    projections over all S rows; out projection, residual, norm2 and FFN over
+    all S rows), the final LayerNorm, and ``blocks_timed`` query blocks spread
+    evenly over the sequence; the layer's attention is their mean times the
+    number of blocks.  With ``full_layer`` the whole layer's attention is run
+    instead (about two minutes).  The full B=32 forward is 32 sequences x
+    (2 layers + final norm): an extrapolation of the measured layer, labelled
+    as such."""
+
     import torch
 
-    from oracle.forward import TransformerConfig, forward, generate_input, xavier_init_weights
+    from oracle.forward import (
+        TransformerConfig,
+        attention_inputs,
+        final_norm,
+        generate_input,
+        layer_output,
+        query_block_rows,
+        xavier_init_weights,
+    )
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(threads)
     w = WORKLOAD
-    lengths = (4096, 8192, 16384, 24576)
-    times = []
+    seq, heads, block = w["seq_len"], w["heads"], 128
+    config = TransformerConfig(1, seq, w["d_model"], heads, w["ffn_dim"], 1, True)
+    state = xavier_init_weights(config, seed=1234)
+    x = generate_input(config, seed=1234)
+    scale = (w["d_model"] // heads) ** -0.5
+    starts = list(range(0, seq, block))
+    if full_layer:
+        chosen = starts
+    else:
+        chosen = [starts[(i * (len(starts) - 1)) // (blocks_timed - 1)] for i in range(blocks_timed)]
     with torch.inference_mode():
-        for seq in lengths:
-            config = TransformerConfig(1, seq, w["d_model"], w["heads"], w["ffn_dim"], 1, True)
-            state = xavier_init_weights(config, seed=1234)
-            x = generate_input(config, seed=1234)
-            forward(state, x[:, :256], TransformerConfig(1, 256, w["d_model"], w["heads"], w["ffn_dim"], 1, True))
-            t0 = time.perf_counter()
-            forward(state, x, config, attention="query_block")
-            times.append(time.perf_counter() - t0)
-    design = np.array([[s, s * s] for s in lengths], dtype=np.float64)
-    (a, b), *_ = np.linalg.lstsq(design, np.array(times), rcond=None)
-    seq = w["seq_len"]
-    per_layer_per_sequence = a * seq + b * seq * seq
-    full_ms = per_layer_per_sequence * w["layers"] * w["batch"] * 1e3
+        small = TransformerConfig(1, 256, w["d_model"], heads, w["ffn_dim"], 1, True)
+        q, k, v = attention_inputs(state, x[:, :256], 0, heads)  # warm the code paths
+        layer_output(state, x[:, :256], query_block_rows(q, k, v, scale, 0, 256), 0)
+        del small
+        t0 = time.perf_counter_ns()
+        q, k, v = attention_inputs(state, x, 0, heads)
+        t_inputs = (time.perf_counter_ns() - t0) / 1e9
+        context = torch.zeros_like(q)
+        # one untimed block at the real size: its first call pays the
+        # allocation of the [H, 128, S] temporaries
+        query_block_rows(q, k, v, scale, chosen[-1], min(chosen[-1] + block, seq))
+        block_times = []
+        for start in chosen:
+            stop = min(start + block, seq)
+            t0 = time.perf_counter_ns()
+            context[..., start:stop, :] = query_block_rows(q, k, v, scale, start, stop)
+            block_times.append((time.perf_counter_ns() - t0) / 1e9)
+        t0 = time.perf_counter_ns()
+        out = layer_output(state, x, context, 0)
+        t_output = (time.perf_counter_ns() - t0) / 1e9
+        t0 = time.perf_counter_ns()
+        final_norm(state, out)
+        t_final = (time.perf_counter_ns() - t0) / 1e9
+    log(f"cpu layer: block times {', '.join(f'{1e3 * t:.0f}' for t in block_times[:8])} ... ms")
+    attention_s = sum(block_times) if full_layer else len(starts) * sum(block_times) / len(block_times)
+    layer_s = t_inputs + attention_s + t_output
+    forward_s = w["batch"] * (w["layers"] * layer_s + t_final)
+    how = ("every query block" if full_layer else
+           f"{len(chosen)} of its {len(starts)} query blocks (each scores all {seq} keys: equal work), "
+           f"mean {1e3 * sum(block_times) / len(block_times):.1f} ms per block")
     return {
-        "value": round(full_ms, 1),
-        "unit": "ms",
-        "cores": threads,
-        "kind": "port",
+        "layer_ms": round(1e3 * layer_s, 1),
+        "forward_ms": round(1e3 * forward_s, 1),
         "sample": (
-            "fp32 oracle forward (official op order, query-blocked attention), one layer of one "
-            f"sequence at D1024 H16 F4096 for S in {list(lengths)} "
-            f"({', '.join(f'{t:.2f}' for t in times)} s); t(S)=a*S+b*S^2 least-squares fit "
-            f"extrapolated to S={seq}, x {w['layers']} layers x {w['batch']} sequences"
+            f"fp32 CPU oracle (official op order, query-blocked attention), one layer of one sequence at "
+            f"S={seq} D{w['d_model']} H{heads} F{w['ffn_dim']}, measured: row-wise work in full "
+            f"({1e3 * (t_inputs + t_output):.0f} ms), attention over {how}, layer {1e3 * layer_s:.0f} ms; "
+            f"the B={w['batch']} forward is an extrapolation: {w['batch']} sequences x ({w['layers']} layers "
+            f"+ final norm {1e3 * t_final:.0f} ms)"
         ),
     }
+
+
+def cpu_configs(threads: int) -> dict:
+    """The CPU oracle (fp32) on BASELINE's other configurations, on the
+    inputs the GPU figures use (16-bit ones widened to fp32): C1 and C2 whole
+    forwards, C3's operators, one layer of one C4 sequence (scaled, labelled).
+    Warm-up and median per the official CPU method."""
+
+    import torch
+
+    from oracle.forward import (
+        TransformerConfig,
+        attention_inputs,
+        default_init_weights,
+        forward,
+        generate_input,
+        layer_output,
+        query_block_causal_attention,
+        xavier_init_weights,
+    )
+    torch.set_num_threads(threads)
+    out = {}
+    with torch.inference_mode():
+        c1 = TransformerConfig(2, 128, 256, 4, 1024, 2, True)
+        state, x = default_init_weights(c1, seed=1234), generate_input(c1, seed=1234)
+        times = _cpu_samples(lambda: forward(state, x, c1), warmup=2, samples=5)
+        out["c1"] = {"ms": round(1e3 * _median(times), 3), "what": "whole forward B2 S128 D256 H4 F1024 L2",
+                     "samples": 5}
+        c2 = TransformerConfig(64, 256, 512, 8, 2048, 4, True)
+        state, x = xavier_init_weights(c2, seed=1234), generate_input(c2, seed=1234)
+        times = _cpu_samples(lambda: forward(state, x, c2), warmup=1, samples=3)
+        out["c2"] = {"ms": round(1e3 * _median(times), 1), "what": "whole forward B64 S256 D512 H8 F2048 L4",
+                     "samples": 3}
+        generator = torch.Generator().manual_seed(1234)
+        q, k, v = ((torch.randn(8, 16, 2048, 64, generator=generator) / 8).to(torch.bfloat16).float()
+                   for _ in range(3))
+        times = _cpu_samples(lambda: query_block_causal_attention(q, k, v, 0.125), warmup=1, samples=5)
+        value = torch.randn(16384, 1024, generator=generator).to(torch.bfloat16).float()
+        update = torch.randn(16384, 1024, generator=generator).to(torch.bfloat16).float()
+        gamma, beta = torch.ones(1024), torch.zeros(1024)
+
+        def boundary():  # the reference's torch boundary: add, then LayerNorm
+            residual = value + update
+            return residual, torch.nn.functional.layer_norm(residual, (1024,), gamma, beta, 1e-5)
+
+        norm_times = _cpu_samples(boundary, warmup=1, samples=5)
+        out["c3"] = {"attention_ms": round(1e3 * _median(times), 2), "norm_ms": round(1e3 * _median(norm_times), 2),
+                     "what": "attention B8 H16 S2048 Dh64 (query-blocked order) and residual add + LayerNorm "
+                             "[16384, 1024], fp32",
+                     "samples": 5}
+        c4 = TransformerConfig(1, 4096, 2048, 32, 8192, 1, True)
+        state, x = xavier_init_weights(c4, seed=1234), generate_input(c4, seed=1234)
+
+        def c4_layer():
+            qq, kk, vv = attention_inputs(state, x, 0, 32)
+            layer_output(state, x, query_block_causal_attention(qq, kk, vv, 0.125), 0)
+
+        times = _cpu_samples(c4_layer, warmup=0, samples=2)
+        layer_ms = 1e3 * _median(times)
+        out["c4"] = {"layer_ms": round(layer_ms, 1), "forward_ms_extrapolated": round(layer_ms * 16 * 2, 1),
+                     "what": "one layer of one sequence S4096 D2048 H32 F8192, measured; the B16 L2 forward "
+                             "is that x 16 sequences x 2 layers (an extrapolation)",
+                     "samples": 2}
+    return out
+
+
+def _deployed_program(d_model: int, seq_len: int):
+    """The committed registry's program for the BASELINE shape of this width
+    and length."""
+
+    from deployment.registry import DEFAULT_DEPLOYED_CONFIGS_PATH
+    from solution.config import ConfigSpec
+
+    document = json.loads(DEFAULT_DEPLOYED_CONFIGS_PATH.read_text(encoding="utf-8"))
+    for bundle in document["bundles"]:
+        for entry in bundle["entries"]:
+            shape = entry["shape"]
+            if shape["qkv_dim"] == d_model and shape["seq_len"] == seq_len and shape["dtype"] == "bfloat16":
+                return ConfigSpec.from_dict(entry["config"])
+    raise RuntimeError(f"no registry entry for D={d_model} S={seq_len}")
+
+
+def _percentile(values, q):
+    ordered = sorted(values)
+    position = (len(ordered) - 1) * q
+    lower, upper = math.floor(position), math.ceil(position)
+    return ordered[lower] + (ordered[upper] - ordered[lower]) * (position - lower)
+
+
+def resident_latency(shape: tuple, *, warmup: int = 20, repeats: int = 100, rounds: int = 3) -> dict:
+    """GPU forward latency of a resident configuration under the reference's
+    formal protocol (benchmarking/protocols.py:116-117: 20 warm-up calls,
+    then 3 rounds of 100; official/torch_transformer_benchmark.py:477-506:
+    events recorded around every call of a round, one synchronization per
+    round), with the registry's program for the shape, bf16, seeded
+    Xavier-uniform weights and N(0,1) input."""
+
+    import torch
+
+    from solution.transformer import UserOptimizedTransformer
+
+    batch, seq, width, heads, ffn, layers = shape
+    device = torch.device("cuda", 0)
+    model = UserOptimizedTransformer(_Config(batch, seq, width, heads, ffn, layers))
+    _init_xavier(model, seed=1234)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    program = _deployed_program(width, seq)
+    model.configure_execution(config=program)
+    generator = torch.Generator(device=device).manual_seed(1234)
+    x = torch.randn(batch, seq, width, generator=generator, device=device, dtype=torch.bfloat16)
+    samples = []
+    with torch.inference_mode():
+        for _ in range(warmup):
+            model(x)
+        torch.cuda.synchronize()
+        for _ in range(rounds):
+            starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+            ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+            for index in range(repeats):
+                starts[index].record()
+                model(x)
+                ends[index].record()
+            torch.cuda.synchronize()
+            samples.extend(a.elapsed_time(b) for a, b in zip(starts, ends))
+    del model, x
+    median = _median(samples)
+    return {
+        "workload": f"B{batch} S{seq} D{width} H{heads} F{ffn} L{layers} bf16",
+        "program": program.config_id,
+        "median_ms": round(median, 4),
+        "p90_ms": round(_percentile(samples, 0.9), 4),
+        "mean_ms": round(sum(samples) / len(samples), 4),
+        "min_ms": round(min(samples), 4),
+        "samples": len(samples),
+        "protocol": f"{warmup} warm-up calls, {rounds} rounds x {repeats} calls, HIP events per call",
+    }
+
+
+def semantic_check(model, x) -> dict:
+    """The measured program's output checked in the same run, as the
+    reference does before it times its long-sequence shape
+    (benchmarking/shape14_measure.py:139-162): one sequence (B=1) at the full
+    length through the program's inner (one-sequence) schedule, against the
+    product's portable reference-order program (query-blocked torch
+    attention, torch norms) run on the GPU in bf16 and in fp32 from the same
+    weights.  ``passed`` is the model-level rule of autotune.accuracy (no less
+    accurate than the bf16 reference path against fp32); the elementwise gates
+    and the reference's continuous ratio (<= 1 passes) are reported beside
+    it."""
+
+    import torch
+
+    from autotune.accuracy import gate_ratio, summarize_errors, summary_no_less_accurate
+    from solution.config import portable_streamed_config
+    from solution.shape14.defaults import hip_streamed_config
+    from solution.transformer import UserOptimizedTransformer
+
+    device = x.device
+    state = model.state_dict()
+    sample = x[:1].contiguous()
+
+    def run(program, dtype):
+        other = UserOptimizedTransformer(model.config)
+        other.load_state_dict(state)
+        other = other.to(device=device, dtype=dtype).eval()
+        other.configure_execution(config=program)
+        with torch.inference_mode():
+            out = other(sample.to(dtype))
+        torch.cuda.synchronize()
+        del other
+        return out.float()
+
+    candidate = run(hip_streamed_config(microbatch_size=1), torch.bfloat16)
+    reference_path = run(portable_streamed_config(), torch.bfloat16)
+    exact = run(portable_streamed_config(), torch.float32)
+    c, r = summarize_errors(candidate, exact), summarize_errors(reference_path, exact)
+    strict = summarize_errors(candidate, reference_path)
+    result = {
+        "what": "B=1 S=100000 forward of the timed weights: HIP program vs the portable program (bf16, fp32)",
+        "passed": summary_no_less_accurate(c, r),
+        "candidate_vs_fp32": {"max_abs": round(c.max_abs, 5), "mean_abs": round(c.mean_abs, 6),
+                              "gate_failures": c.outside},
+        "reference_path_vs_fp32": {"max_abs": round(r.max_abs, 5), "mean_abs": round(r.mean_abs, 6),
+                                   "gate_failures": r.outside},
+        "candidate_vs_reference_path": {"max_abs": round(strict.max_abs, 5), "gate_failures": strict.outside,
+                                        "elements": strict.total},
+        "gate_ratio_2e-2_1e-2": round(gate_ratio(candidate, reference_path, atol=2e-2, rtol=1e-2), 4),
+        "official_ratio_rtol0.02_atol0.002": round(
+            gate_ratio(candidate, reference_path, atol=0.002, rtol=0.02), 4),
+    }
+    del candidate, reference_path, exact
+    torch.cuda.empty_cache()
+    log(f"semantic check: passed={result['passed']} candidate max_abs {c.max_abs:.4g} vs reference path "
+        f"{r.max_abs:.4g} (against fp32)")
+    return result
 
 
 def main() -> int:
@@ -615,6 +896,11 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-check", action="store_true", help="skip the in-run B=1 semantic check")
+    parser.add_argument("--no-resident", action="store_true",
+                        help="skip the C2 / C4 latency and the CPU figures of the other configurations")
+    parser.add_argument("--cpu-full-layer", action="store_true",
+                        help="time every query block of the CPU layer at S=100000 (about two minutes)")
     parser.add_argument("--no-config3", action="store_true",
                         help="skip the operator-alone figures (e.g. for a kernel trace of the forward alone)")
     parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
@@ -641,10 +927,32 @@ def main() -> int:
     # The operators alone first: directly after the forward the chip runs hot
     # and its clock is lower (attention 114 us there against ~102 us here).
     config3 = None if args.no_config3 else config3_summary()
-    gpu = gpu_benchmark(args.steps, args.warmup)
-    baseline = None if args.no_cpu_baseline else cpu_baseline()
-    if baseline is not None:
-        log(f"cpu baseline: {baseline['value'] / 1e3:.0f} s per forward on {baseline['cores']} threads")
+    gpu = gpu_benchmark(args.steps, args.warmup, check=not args.no_check)
+    resident = None
+    if not args.no_resident:
+        resident = {"c2": resident_latency((64, 256, 512, 8, 2048, 4)),
+                    "c4": resident_latency((16, 4096, 2048, 32, 8192, 2))}
+        log(f"resident: C2 {resident['c2']['median_ms']} ms, C4 {resident['c4']['median_ms']} ms (median)")
+    threads, affinity, quota = _cpu_cores()
+    baseline = None
+    cpu_other = None
+    if not args.no_cpu_baseline:
+        long_sequence = cpu_long_sequence(threads, full_layer=args.cpu_full_layer)
+        baseline = {
+            "value": long_sequence["forward_ms"],
+            "unit": "ms",
+            "cores": threads,
+            "kind": "port",
+            "sample": long_sequence["sample"],
+            "measured_layer_ms": long_sequence["layer_ms"],
+            "forward_is_extrapolated": True,
+            "affinity_cpus": affinity,
+            "cgroup_cpu_quota": quota,
+        }
+        log(f"cpu baseline: layer {long_sequence['layer_ms'] / 1e3:.1f} s measured, forward "
+            f"{baseline['value'] / 1e3:.0f} s extrapolated, {threads} threads")
+        if not args.no_resident:
+            cpu_other = cpu_configs(threads)
     achieved = gpu["attention_tflops"]
     traffic = measured_traffic()
     record = {
@@ -697,7 +1005,10 @@ def main() -> int:
             "traffic": traffic,
         },
         "cpu_baseline": baseline,
+        "semantic_check": gpu.get("semantic_check"),
         "config3": config3,
+        "resident_gpu": resident,
+        "cpu_configs": cpu_other,
     }
     print(json.dumps(record), flush=True)
     return 0

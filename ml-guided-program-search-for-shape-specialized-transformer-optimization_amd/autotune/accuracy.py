@@ -76,6 +76,31 @@ def summarize_errors(
     )
 
 
+def gate_ratio(output: torch.Tensor, reference: torch.Tensor, *, atol: float, rtol: float) -> float:
+    """How far ``output`` is from failing the elementwise OR gate: the largest
+    over elements of min(|err| / atol, |err| / (rtol |ref|)), so the gate
+    passes exactly when the ratio is at most 1 (the continuous figure the
+    reference reports with its measurements,
+    benchmarking/measurement_core.py:182-224).  An element with a zero
+    allowance counts 0 when its error is 0 and infinity otherwise; a
+    non-finite element makes the ratio infinite."""
+
+    out = output.detach().float()
+    ref = reference.detach().float().to(out.device)
+    if out.shape != ref.shape:
+        return float("inf")
+    if out.numel() == 0:
+        return 0.0
+    if not bool((torch.isfinite(out) & torch.isfinite(ref)).all()):
+        return float("inf")
+    err = (out - ref).abs()
+    zero_rule = torch.where(err == 0, torch.zeros_like(err), torch.full_like(err, float("inf")))
+    absolute = err / atol if atol > 0 else zero_rule
+    allowance = rtol * ref.abs()
+    relative = torch.where(allowance > 0, err / allowance.clamp_min(torch.finfo(torch.float32).tiny), zero_rule)
+    return float(torch.minimum(absolute, relative).max())
+
+
 def summary_no_less_accurate(candidate: ErrorSummary, incumbent: ErrorSummary) -> bool:
     """The rule above on precomputed summaries (same reference, same shape)."""
 
@@ -103,6 +128,7 @@ __all__ = [
     "ErrorSummary",
     "GATE_ATOL",
     "GATE_RTOL",
+    "gate_ratio",
     "no_less_accurate",
     "summarize_errors",
     "summary_no_less_accurate",

@@ -193,18 +193,28 @@ def query_block_causal_attention(
     temporaries (no key-side causal skipping, like the reference)."""
 
     seq = q.shape[-2]
-    key_positions = torch.arange(seq)
-    k_t = k.transpose(-2, -1)
-    chunks = []
-    for start in range(0, seq, query_block):
-        stop = min(start + query_block, seq)
-        scores = torch.matmul(q[..., start:stop, :], k_t)
-        scores.mul_(scale)
-        query_positions = torch.arange(start, stop)
-        scores.masked_fill_(key_positions[None, :] > query_positions[:, None], float("-inf"))
-        probs = torch.softmax(scores.float(), dim=-1).to(q.dtype)
-        chunks.append(torch.matmul(probs, v))
-    return torch.cat(chunks, dim=-2)
+    return torch.cat(
+        [query_block_rows(q, k, v, scale, start, min(start + query_block, seq))
+         for start in range(0, seq, query_block)],
+        dim=-2,
+    )
+
+
+def query_block_rows(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, start: int, stop: int
+) -> torch.Tensor:
+    """Query rows [start, stop) in the order of solution/operators/attention/
+    sdpa.py:116-170: scores against every key, scale, causal -inf mask, fp32
+    softmax cast to the input dtype, then P V.  Every block does the same
+    work, whatever its position (no key-side causal skipping)."""
+
+    key_positions = torch.arange(q.shape[-2])
+    scores = torch.matmul(q[..., start:stop, :], k.transpose(-2, -1))
+    scores.mul_(scale)
+    query_positions = torch.arange(start, stop)
+    scores.masked_fill_(key_positions[None, :] > query_positions[:, None], float("-inf"))
+    probs = torch.softmax(scores.float(), dim=-1).to(q.dtype)
+    return torch.matmul(probs, v)
 
 
 def causal_attention_rows(
@@ -271,31 +281,49 @@ def forward(
         attention == "auto" and x.shape[1] > 4096
     )
     attend = query_block_causal_attention if use_blocks else dense_causal_attention
-    batch, seq, width = x.shape
     for index in range(config.num_layers):
-        keys = _layer_keys(index)
-        normalized = _layer_norm(x, state, keys["norm1"])
-        q = _split_heads(_linear(normalized, state, keys["q"]), heads)
-        k = _split_heads(_linear(normalized, state, keys["k"]), heads)
-        v = _split_heads(_linear(normalized, state, keys["v"]), heads)
-        context = attend(q, k, v, scale)
-        context = context.transpose(1, 2).contiguous().view(batch, seq, width)
-        x = x + _linear(context, state, keys["out"])
-        hidden = F.gelu(_linear(_layer_norm(x, state, keys["norm2"]), state, keys["ffn_in"]), approximate="none")
-        x = x + _linear(hidden, state, keys["ffn_out"])
+        q, k, v = attention_inputs(state, x, index, heads)
+        x = layer_output(state, x, attend(q, k, v, scale), index)
+    return final_norm(state, x)
+
+
+def attention_inputs(
+    state: dict[str, torch.Tensor], x: torch.Tensor, index: int, heads: int
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Layer ``index`` up to the attention: norm1, then the q, k and v
+    projections split into [B, H, S, Dh] (official :98-106)."""
+
+    keys = _layer_keys(index)
+    normalized = _layer_norm(x, state, keys["norm1"])
+    return tuple(_split_heads(_linear(normalized, state, keys[name]), heads) for name in ("q", "k", "v"))
+
+
+def layer_output(
+    state: dict[str, torch.Tensor], x: torch.Tensor, context: torch.Tensor, index: int
+) -> torch.Tensor:
+    """Layer ``index`` after the attention: context [B, H, S, Dh] back to
+    [B, S, D], out projection and residual, then norm2, FFN with exact GELU
+    and residual (official :112-141)."""
+
+    keys = _layer_keys(index)
+    batch, seq, width = x.shape
+    context = context.transpose(1, 2).contiguous().view(batch, seq, width)
+    x = x + _linear(context, state, keys["out"])
+    hidden = F.gelu(_linear(_layer_norm(x, state, keys["norm2"]), state, keys["ffn_in"]), approximate="none")
+    return x + _linear(hidden, state, keys["ffn_out"])
+
+
+def final_norm(state: dict[str, torch.Tensor], x: torch.Tensor) -> torch.Tensor:
+    """The model's last LayerNorm (official :169)."""
+
     return _layer_norm(x, state, "final_norm")
-
-
-def layer_forward_flops(config: TransformerConfig, rows: int, attended_keys: int) -> int:
-    """Multiply-add FLOPs of one layer for ``rows`` query rows that attend to
-    ``attended_keys`` keys in total (used to scale CPU baseline samples)."""
-
-    d, f = config.d_model, config.ffn_dim
-    return 2 * rows * (4 * d * d + 2 * d * f) + 4 * attended_keys * d
 
 
 __all__ = [
     "LAYER_NORM_EPS",
+    "attention_inputs",
+    "final_norm",
+    "layer_output",
     "TransformerConfig",
     "cast_state",
     "causal_attention_rows",
@@ -303,7 +331,7 @@ __all__ = [
     "dense_causal_attention",
     "forward",
     "generate_input",
-    "layer_forward_flops",
     "query_block_causal_attention",
+    "query_block_rows",
     "xavier_init_weights",
 ]

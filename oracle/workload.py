@@ -59,10 +59,6 @@ def residual_norm_bytes(
     return rows * width * (value + update + residual + normalized) + 2 * width * params
 
 
-def norm_bytes(rows: int, width: int, *, value: int = 2, normalized: int = 2, params: int = 2) -> int:
-    return rows * width * (value + normalized) + 2 * width * params
-
-
 __all__ = [
     "C1",
     "C2",
@@ -73,6 +69,5 @@ __all__ = [
     "Workload",
     "causal_attention_flops",
     "estimated_model_flops",
-    "norm_bytes",
     "residual_norm_bytes",
 ]

@@ -25,6 +25,7 @@ from oracle.forward import (
     forward,
     generate_input,
     query_block_causal_attention,
+    query_block_rows,
     xavier_init_weights,
 )
 from oracle.workload import (
@@ -72,6 +73,9 @@ def test_query_block_order_equals_dense_order():
     dense = dense_causal_attention(q, k, v, 0.25)
     for block in (1, 7, 128, 300, 512):
         torch.testing.assert_close(query_block_causal_attention(q, k, v, 0.25, query_block=block), dense)
+    # one block anywhere in the sequence (the CPU baseline times sampled blocks)
+    torch.testing.assert_close(query_block_rows(q, k, v, 0.25, 37, 101), dense[..., 37:101, :])
+    torch.testing.assert_close(query_block_rows(q, k, v, 0.25, 299, 300), dense[..., 299:, :])
 
 
 def test_attention_matches_torch_sdpa_float64():
@@ -314,3 +318,25 @@ def test_launch_search_gate_is_the_model_parity_rule():
     incumbent = _noisy(exact, 0.01, 4)
     for candidate in (_noisy(exact, 0.01, 5), _noisy(exact, 0.015, 5), _noisy(exact, 0.03, 5)):
         assert no_less_accurate(candidate, incumbent, exact) == model_parity(exact, incumbent, candidate).passed
+
+
+def test_gate_ratio_is_at_most_one_exactly_when_the_gate_passes():
+    from autotune.accuracy import gate_ratio, summarize_errors
+
+    reference = torch.tensor([1.0, 5.0, -5.0, 0.0])
+    # allowances: max(0.02, 0.01 |ref|) = 0.02, 0.05, 0.05, 0.02
+    output = torch.tensor([1.01, 5.03, -5.04, 0.005])
+    assert gate_ratio(output, reference, atol=0.02, rtol=0.01) == pytest.approx(0.8, rel=1e-4)
+    assert summarize_errors(output, reference).outside == 0
+    failing = torch.tensor([1.03, 5.0, -5.0, 0.0])  # 0.03 / 0.02
+    assert gate_ratio(failing, reference, atol=0.02, rtol=0.01) == pytest.approx(1.5, rel=1e-4)
+    assert summarize_errors(failing, reference).outside == 1
+    # a zero allowance: exact elements count 0, others infinity
+    assert gate_ratio(torch.zeros(3), torch.zeros(3), atol=0.0, rtol=0.01) == 0.0
+    assert gate_ratio(torch.tensor([1e-6]), torch.zeros(1), atol=0.0, rtol=0.01) == float("inf")
+    assert gate_ratio(torch.tensor([float("nan")]), torch.ones(1), atol=0.02, rtol=0.01) == float("inf")
+    generator = torch.Generator().manual_seed(9)
+    ref = torch.randn(1000, generator=generator)
+    out = ref + 0.03 * torch.randn(1000, generator=generator)
+    ratio = gate_ratio(out, ref, atol=0.02, rtol=0.01)
+    assert (ratio <= 1.0) == (summarize_errors(out, ref).outside == 0)
