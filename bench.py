@@ -22,7 +22,7 @@ the attention on query blocks spread over the sequence (every block scores
 all keys, so all blocks cost the same); ``value`` scales that measured layer
 to the B=32 two-layer forward, an extrapolation labelled as such.
 ``cpu_configs`` times the CPU oracle on BASELINE's other configurations
-(C1, C2 whole; C3's operators; one C4 layer).
+(C1, C2 and C4 whole; C3's operators).
 
 ``semantic_check`` compares, in the same run, one sequence of the timed
 weights through the HIP program with the product's portable program on the
@@ -696,20 +696,18 @@ def cpu_long_sequence(threads: int, *, blocks_timed: int = 24, full_layer: bool 
 
 
 def cpu_configs(threads: int) -> dict:
-    """The CPU oracle (fp32) on BASELINE's other configurations, on the
-    inputs the GPU figures use (16-bit ones widened to fp32): C1 and C2 whole
-    forwards, C3's operators, one layer of one C4 sequence (scaled, labelled).
-    Warm-up and median per the official CPU method."""
+    """The CPU oracle (fp32) on BASELINE's other configurations: C1, C2 and C4
+    whole forwards and C3's operators (on inputs widened from the bf16 ones
+    the GPU figures use).  Warm-up and median per the official CPU method
+    where a sample takes seconds; C4 (about 20 s) is one sample."""
 
     import torch
 
     from oracle.forward import (
         TransformerConfig,
-        attention_inputs,
         default_init_weights,
         forward,
         generate_input,
-        layer_output,
         query_block_causal_attention,
         xavier_init_weights,
     )
@@ -743,19 +741,12 @@ def cpu_configs(threads: int) -> dict:
                      "what": "attention B8 H16 S2048 Dh64 (query-blocked order) and residual add + LayerNorm "
                              "[16384, 1024], fp32",
                      "samples": 5}
-        c4 = TransformerConfig(1, 4096, 2048, 32, 8192, 1, True)
+        # C4 in full (about 20 s on 16 host threads), one sample
+        c4 = TransformerConfig(16, 4096, 2048, 32, 8192, 2, True)
         state, x = xavier_init_weights(c4, seed=1234), generate_input(c4, seed=1234)
-
-        def c4_layer():
-            qq, kk, vv = attention_inputs(state, x, 0, 32)
-            layer_output(state, x, query_block_causal_attention(qq, kk, vv, 0.125), 0)
-
-        times = _cpu_samples(c4_layer, warmup=0, samples=2)
-        layer_ms = 1e3 * _median(times)
-        out["c4"] = {"layer_ms": round(layer_ms, 1), "forward_ms_extrapolated": round(layer_ms * 16 * 2, 1),
-                     "what": "one layer of one sequence S4096 D2048 H32 F8192, measured; the B16 L2 forward "
-                             "is that x 16 sequences x 2 layers (an extrapolation)",
-                     "samples": 2}
+        times = _cpu_samples(lambda: forward(state, x, c4, attention="query_block"), warmup=0, samples=1)
+        out["c4"] = {"ms": round(1e3 * times[0], 1),
+                     "what": "whole forward B16 S4096 D2048 H32 F8192 L2 (query-blocked order)", "samples": 1}
     return out
 
 

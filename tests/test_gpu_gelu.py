@@ -9,6 +9,8 @@ pass the 16-bit gate of oracle.compare.
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -43,6 +45,33 @@ def test_exact_gelu_matches_float64(gpu_device, n, dtype):
     torch.cuda.synchronize()
     assert marker == "hip_exact_gelu" and y.dtype == dtype and y.shape == x.shape
     _check(x, y, dtype, f"gelu n={n} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_negative_tail_within_one_ulp(gpu_device, dtype):
+    """v in [-10, -3]: GELU(v) is 1e-23 .. 4e-3, and the result must stay
+    within one ulp RELATIVE to float64 exact GELU (no absolute slack beyond
+    half the dtype's smallest subnormal step).  An erfc approximation with
+    only an absolute error bound fails this by 1-2% below v = -5."""
+
+    from solution.kernels.ffn import prevalidated_hip_exact_gelu
+
+    x = torch.linspace(-10.0, -3.0, 70001).to(dtype)
+    with torch.inference_mode():
+        y, _ = prevalidated_hip_exact_gelu(x.to(gpu_device))
+    torch.cuda.synchronize()
+    # v * erfc(-v / sqrt 2) / 2 in float64: torch's float64 GELU forms
+    # 1 + erf(v / sqrt 2), which cancels to 0 below v = -8.3
+    xd = x.double()
+    reference = xd * 0.5 * torch.special.erfc(-xd / math.sqrt(2.0))
+    assert bool((reference < 0).all())
+    ulp = 2.0**-7 if dtype == torch.bfloat16 else 2.0**-10
+    tiny = 2.0**-134 if dtype == torch.bfloat16 else 2.0**-25
+    err = (y.cpu().double() - reference).abs()
+    rel = (err / reference.abs()).max().item()
+    print(f"negative tail {dtype}: max relative error {rel:.3g}", flush=True)
+    assert bool((err <= ulp * reference.abs() + tiny).all()), (
+        f"{int((err > ulp * reference.abs() + tiny).sum())} tail elements above one ulp (max rel {rel:.3g})")
 
 
 @pytest.mark.parametrize("launch", [(512, 1), (1024, 2), (4096, 4), (8192, 8), (16384, 4)])
