@@ -279,6 +279,44 @@ int sah_qkv_projection(
     int dtype, int block_m, int block_n, int block_k, int num_warps,
     sah_stream_t stream);
 
+/*
+ * The model's first LayerNorm fused into the packed QKV projection:
+ *   y   = round_to(dtype, (x - mean) * rstd * ln_weight + ln_bias)
+ *         (mean, rstd = 1 / sqrt(var + ln_eps) of each x row in fp32, biased
+ *          variance; y stays on chip)
+ *   qkv = round_to(dtype, y weight^T + bias), stored as sah_qkv_projection does.
+ * The row statistics are formed exactly as sah_norm forms them, so the outputs
+ * equal those of sah_norm (LayerNorm, same weight, bias, eps, dtype) followed
+ * by sah_qkv_projection, bit for bit.  Two launches on the stream: the row
+ * statistics (mean, rstd as two floats per row) into the workspace, then the
+ * projection, which normalizes x as it stages it.
+ *
+ * Replaces the reference's
+ *   _initial_norm_qkv_native_bhsd_kernel + the fused initial-norm QKV launch
+ *     (solution/kernels/projection/triton_shape07_initial_norm_qkv.py:67-140,
+ *      173-218), which the reference plans as initial_norm TRITON_FUSED_QKV
+ *      (solution/plan_builder.py:1097-1160) and calls for layer 0
+ *      (solution/transformer.py:1364-1440).
+ * Arguments as sah_qkv_projection, plus ln_weight / ln_bias: [d_model] in
+ * dtype, 16-byte aligned, both required; ln_eps finite and >= 0; workspace:
+ * device memory of at least sah_norm_qkv_workspace_bytes(batch, seq_len)
+ * bytes, 16-byte aligned, else SAH_ERR_WORKSPACE before any launch (it only
+ * carries the statistics between the two launches; calls that share one
+ * workspace must not overlap).  d_model must be 512, 1024, 2048 or 4096.
+ */
+int sah_norm_qkv_projection(
+    const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+    const void* weight, const void* bias,
+    void* query, void* key, void* value,
+    int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads,
+    int64_t x_row_stride, int value_layout, int64_t value_seq_stride,
+    int dtype, int block_m, int block_n, int block_k, int num_warps,
+    void* workspace, size_t workspace_bytes, sah_stream_t stream);
+
+/* Workspace sah_norm_qkv_projection needs: 8 bytes per token (0 for an empty
+ * or invalid size). */
+size_t sah_norm_qkv_workspace_bytes(int64_t batch, int64_t seq_len);
+
 /* 1 if sah_qkv_projection implements the launch, else 0 (mirrors the
  * reference's _launch_config_is_valid,
  * solution/kernels/projection/triton_qkv_layout.py:29-43). */

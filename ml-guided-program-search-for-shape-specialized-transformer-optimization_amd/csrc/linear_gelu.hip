@@ -30,6 +30,19 @@
 // intermediate).  The value may instead be written seq-contiguous,
 // [B, H, head_dim, v_ld], the layout the attention kernel reads its V^T
 // operand from, which saves the attention's own transpose pass.
+//
+// With a LayerNorm prologue (sah_norm_qkv_projection) the projection also
+// fuses the model's first LayerNorm, the reference's initial-norm / QKV fusion
+// (solution/kernels/projection/triton_shape07_initial_norm_qkv.py:67-140):
+// a row-statistics kernel first forms each row's fp32 mean and 1/std into a
+// workspace (8 bytes per row; one wavefront per row with the lane mapping,
+// per-lane Welford state and pairwise merge of the fused norm kernel, so the
+// statistics are those of sah_norm bit for bit), then the projection
+// normalizes x as each K step is staged into LDS, rounding the normalized
+// row to the model dtype before the MFMAs as the unfused boundary rounds its
+// output.  The normalized rows never reach HBM.  (Forming the statistics
+// inside the projection instead makes each of the 3 d_model / 256 column
+// tiles of a row block re-read the whole block before its first MFMA.)
 
 #include <cmath>
 
@@ -70,7 +83,95 @@ struct LinearParams {
   int seq_len, heads, head_dim, d_model;
   int v_seq_major;   // value as [B][H][head_dim][v_ld] instead of [B][H][S][head_dim]
   int seq_aligned;   // seq_len % 8 == 0: 8-token runs never cross a sequence
+  // LayerNorm on the x rows: weight / bias [K] in the x dtype and each
+  // row's (mean, 1/std).
+  const void* ln_w;
+  const void* ln_b;
+  const float2* ln_stats;
 };
+
+// Row statistics of G rows of K = ITERS * 512 elements by one wavefront,
+// exactly as the fused norm kernel forms them: lane l holds elements
+// (i * 64 + l) * 8 .. + 7 of a row, a per-lane mean then M2, merged across
+// the wave.
+template <typename T, int ITERS, int G>
+__device__ __forceinline__ void group_stats(const u32x4 (*raw)[ITERS], float eps, float2* out) {
+  constexpr int N = ITERS * 8;
+  float mean[G], m2[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float v[N];
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) unpack8<T>(raw[g][i], v + 8 * i);
+    float lane_mean = 0.0f;
+#pragma unroll
+    for (int e = 0; e < N; ++e) lane_mean += v[e];
+    lane_mean *= (1.0f / N);
+    float lane_m2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const float d = v[e] - lane_mean;
+      lane_m2 += d * d;
+    }
+    mean[g] = lane_mean;
+    m2[g] = lane_m2;
+  }
+  wave_welford_rows<G>(mean, m2, (float)N);
+#pragma unroll
+  for (int g = 0; g < G; ++g) out[g] = make_float2(mean[g], rsqrtf(m2[g] * (1.0f / (N * 64)) + eps));
+}
+
+// (mean, 1/std) of every row of x [rows][K] into stats[rows]: wavefront w
+// of a workgroup owns G consecutive rows, loads all of them, then forms their
+// statistics together (the row loads and the cross-lane merges of the G
+// rows overlap).
+constexpr int kStatsWaves = 4;
+template <typename T, int ITERS>
+__global__ __launch_bounds__(kStatsWaves * 64) void row_stats_kernel(const T* x, int64_t x_ld,
+                                                                      int64_t rows, float eps,
+                                                                      float2* stats) {
+  constexpr int G = 16 / ITERS;  // 64 VGPRs of row data per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t first = ((int64_t)blockIdx.x * kStatsWaves + (threadIdx.x >> 6)) * G;
+  if (first >= rows) return;  // wave-uniform; the kernel has no barrier
+  u32x4 raw[G][ITERS];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    // rows past the end read the group's first row (in bounds), never stored
+    const T* rp = x + (first + g < rows ? first + g : first) * x_ld;
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) raw[g][i] = load16(rp + (i * 64 + lane) * 8);
+  }
+  float2 st[G];
+  group_stats<T, ITERS, G>(raw, eps, st);
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (first + g < rows) stats[first + g] = st[g];
+  }
+}
+
+template <typename T, int ITERS>
+int launch_row_stats(const T* x, int64_t x_ld, int64_t rows, float eps, float2* stats,
+                     hipStream_t stream) {
+  constexpr int64_t rows_per_block = kStatsWaves * (16 / ITERS);
+  const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((row_stats_kernel<T, ITERS>), dim3((unsigned)blocks), dim3(kStatsWaves * 64), 0,
+                     stream, x, x_ld, rows, eps, stats);
+  return check_hip(hipGetLastError(), "row statistics kernel launch");
+}
+
+template <typename T>
+int row_stats(const void* x, int64_t x_ld, int64_t rows, int64_t k, float eps, float2* stats,
+              hipStream_t stream) {
+  const T* xt = static_cast<const T*>(x);
+  switch (k) {
+    case 512: return launch_row_stats<T, 1>(xt, x_ld, rows, eps, stats, stream);
+    case 1024: return launch_row_stats<T, 2>(xt, x_ld, rows, eps, stats, stream);
+    case 2048: return launch_row_stats<T, 4>(xt, x_ld, rows, eps, stats, stream);
+    default: return launch_row_stats<T, 8>(xt, x_ld, rows, eps, stats, stream);
+  }
+}
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -79,7 +180,7 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool LN = false>
 __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
@@ -117,9 +218,27 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   const T* xg = static_cast<const T*>(p.x);
   const T* wg = static_cast<const T*>(p.w);
 
+  // ---- LayerNorm: the (mean, 1/std) of the 4 rows this thread stages.
+  float ln_mean[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ln_rstd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (LN) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = m0 + ((tid + kThreads * i) >> 3);
+      if (m < p.rows) {
+        const float2 st = p.ln_stats[m];
+        ln_mean[i] = st.x;
+        ln_rstd[i] = st.y;
+      }
+    }
+  }
+  const T* lnw = static_cast<const T*>(p.ln_w);
+  const T* lnb = static_cast<const T*>(p.ln_b);
+
   // ---- staging: 4 chunks of 16 bytes of x and of W per thread and K step.
-  // Chunk c = tid + kThreads * i is row c / 8, elements 8 (c % 8) .. + 7.
+  // Chunk c = tid + kThreads * i is row c / 8, elements 8 (c % 8) .. + 7
+  // (the same 8 columns for all four chunks of a thread).
   u32x4 x_pref[4], w_pref[4];
+  u32x4 lnw_pref = {0u, 0u, 0u, 0u}, lnb_pref = {0u, 0u, 0u, 0u};
   auto load_step = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -132,14 +251,33 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
       x_pref[i] = raw;
       w_pref[i] = load16(wg + (int64_t)(n0 + row) * p.k + k0 + kc);
     }
+    if constexpr (LN) {
+      const int kc = (tid & 7) * 8;
+      lnw_pref = load16(lnw + k0 + kc);
+      lnb_pref = load16(lnb + k0 + kc);
+    }
   };
   auto store_step = [&](int stage) {
+    float lw[8], lb[8];
+    if constexpr (LN) {
+      unpack8<T>(lnw_pref, lw);
+      unpack8<T>(lnb_pref, lb);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + kThreads * i;
       const int row = c >> 3;
       const int kc = (c & 7) * 8;
-      *reinterpret_cast<u32x4*>(&x_lds[stage][row][kc]) = x_pref[i];
+      u32x4 xs = x_pref[i];
+      if constexpr (LN) {
+        // the fused norm kernel's expression, rounded to T from fp32 as it does
+        float v[8], y[8];
+        unpack8<T>(xs, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = fp32_result<T>((v[e] - ln_mean[i]) * ln_rstd[i] * lw[e] + lb[e]);
+        xs = pack8<T>(y);
+      }
+      *reinterpret_cast<u32x4*>(&x_lds[stage][row][kc]) = xs;
       *reinterpret_cast<u32x4*>(&w_lds[stage][row][kc]) = w_pref[i];
     }
   };
@@ -283,9 +421,9 @@ __global__ __launch_bounds__(kThreads) void linear_kernel(LinearParams p) {
   }
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool LN = false>
 int launch_linear(const LinearParams& prm, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_kernel<T, EPI>), dim3(prm.num_tiles), dim3(kThreads), 0, stream, prm);
+  hipLaunchKernelGGL((linear_kernel<T, EPI, LN>), dim3(prm.num_tiles), dim3(kThreads), 0, stream, prm);
   return check_hip(hipGetLastError(), "linear kernel launch");
 }
 
@@ -362,53 +500,70 @@ extern "C" int sah_qkv_launch_supported(int block_m, int block_n, int block_k, i
   return block_m == kBM && block_n == kBN && block_k == kBK && num_warps == kWaves;
 }
 
-extern "C" int sah_qkv_projection(const void* x, const void* weight, const void* bias, void* query,
-                                  void* key, void* value, int64_t batch, int64_t seq_len,
-                                  int64_t d_model, int64_t heads, int64_t x_row_stride,
-                                  int value_layout, int64_t value_seq_stride, int dtype,
-                                  int block_m, int block_n, int block_k, int num_warps,
-                                  sah_stream_t stream) {
+namespace {
+int qkv_projection(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                   const void* weight, const void* bias, void* query, void* key, void* value,
+                   int64_t batch, int64_t seq_len, int64_t d_model, int64_t heads,
+                   int64_t x_row_stride, int value_layout, int64_t value_seq_stride, int dtype,
+                   int block_m, int block_n, int block_k, int num_warps, void* workspace,
+                   size_t workspace_bytes, sah_stream_t stream) {
+  const bool ln = ln_weight != nullptr || ln_bias != nullptr;
+  const char* entry = ln ? "sah_norm_qkv_projection" : "sah_qkv_projection";
   if (!sah_qkv_launch_supported(block_m, block_n, block_k, num_warps))
-    return fail(SAH_ERR_UNSUPPORTED,
-                "sah_qkv_projection: launch (%d, %d, %d, %d) is not implemented (256, 256, 64, 8)",
-                block_m, block_n, block_k, num_warps);
+    return fail(SAH_ERR_UNSUPPORTED, "%s: launch (%d, %d, %d, %d) is not implemented (256, 256, 64, 8)",
+                entry, block_m, block_n, block_k, num_warps);
   if (dtype != SAH_DTYPE_BF16 && dtype != SAH_DTYPE_F16)
-    return fail(SAH_ERR_UNSUPPORTED, "sah_qkv_projection: dtype %d is not bf16 or f16", dtype);
+    return fail(SAH_ERR_UNSUPPORTED, "%s: dtype %d is not bf16 or f16", entry, dtype);
   if (value_layout != SAH_QKV_VALUE_BHSD && value_layout != SAH_QKV_VALUE_SEQ_MAJOR)
-    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_qkv_projection: unknown value layout %d", value_layout);
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: unknown value layout %d", entry, value_layout);
   if (batch < 0 || seq_len <= 0 || d_model <= 0 || heads <= 0)
-    return fail(SAH_ERR_INVALID_ARGUMENT,
-                "sah_qkv_projection: bad sizes batch=%lld seq_len=%lld d_model=%lld heads=%lld",
-                (long long)batch, (long long)seq_len, (long long)d_model, (long long)heads);
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: bad sizes batch=%lld seq_len=%lld d_model=%lld heads=%lld",
+                entry, (long long)batch, (long long)seq_len, (long long)d_model, (long long)heads);
   if (d_model % kBN != 0 || d_model > (1 << 18) || d_model % heads != 0 || (d_model / heads) % 8 != 0)
-    return fail(SAH_ERR_UNSUPPORTED,
-                "sah_qkv_projection: d_model must be a multiple of %d (at most 2^18) and split "
+    return fail(SAH_ERR_UNSUPPORTED, "%s: d_model must be a multiple of %d (at most 2^18) and split "
                 "into heads of a multiple of 8 elements (got d_model %lld, %lld heads)",
-                kBN, (long long)d_model, (long long)heads);
+                entry, kBN, (long long)d_model, (long long)heads);
   if (x_row_stride < d_model || x_row_stride % 8 != 0)
-    return fail(SAH_ERR_INVALID_ARGUMENT,
-                "sah_qkv_projection: x row stride %lld must cover d_model and be a multiple of 8",
-                (long long)x_row_stride);
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: x row stride %lld must cover d_model and be a multiple of 8",
+                entry, (long long)x_row_stride);
   if (value_layout == SAH_QKV_VALUE_SEQ_MAJOR && (value_seq_stride < seq_len || value_seq_stride % 8 != 0))
-    return fail(SAH_ERR_INVALID_ARGUMENT,
-                "sah_qkv_projection: value seq stride %lld must cover seq_len %lld and be a "
-                "multiple of 8",
-                (long long)value_seq_stride, (long long)seq_len);
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: value seq stride %lld must cover seq_len %lld and be a "
+                "multiple of 8", entry, (long long)value_seq_stride, (long long)seq_len);
+  if (ln) {
+    if (ln_weight == nullptr || ln_bias == nullptr)
+      return fail(SAH_ERR_INVALID_ARGUMENT, "%s: LayerNorm weight and bias are both required", entry);
+    if (!aligned16(ln_weight) || !aligned16(ln_bias))
+      return fail(SAH_ERR_INVALID_ARGUMENT, "%s: LayerNorm weight and bias must be 16-byte aligned",
+                  entry);
+    if (!(std::isfinite(ln_eps) && ln_eps >= 0.0f))
+      return fail(SAH_ERR_INVALID_ARGUMENT, "%s: eps must be finite and non-negative", entry);
+    if (d_model != 512 && d_model != 1024 && d_model != 2048 && d_model != 4096)
+      return fail(SAH_ERR_UNSUPPORTED, "%s: d_model must be 512, 1024, 2048 or 4096 (got %lld)", entry,
+                  (long long)d_model);
+  }
   if (batch == 0) return SAH_OK;
   if (seq_len > INT32_MAX || batch > INT32_MAX / seq_len)
-    return fail(SAH_ERR_UNSUPPORTED, "sah_qkv_projection: batch x seq_len must be below 2^31");
+    return fail(SAH_ERR_UNSUPPORTED, "%s: batch x seq_len must be below 2^31", entry);
   if (x == nullptr || weight == nullptr || query == nullptr || key == nullptr || value == nullptr)
-    return fail(SAH_ERR_INVALID_ARGUMENT, "sah_qkv_projection: null tensor pointer");
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", entry);
   if (!aligned16(x) || !aligned16(weight) || !aligned16(query) || !aligned16(key) || !aligned16(value) ||
       (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 7u) != 0))
-    return fail(SAH_ERR_INVALID_ARGUMENT,
-                "sah_qkv_projection: x, weight, query, key and value must be 16-byte aligned, "
-                "bias 8-byte aligned");
+    return fail(SAH_ERR_INVALID_ARGUMENT, "%s: x, weight, query, key and value must be 16-byte aligned, "
+                "bias 8-byte aligned", entry);
   const int64_t rows = batch * seq_len;
+  if (ln) {
+    const size_t need = sah_norm_qkv_workspace_bytes(batch, seq_len);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace))
+      return fail(SAH_ERR_WORKSPACE, "%s: needs a 16-byte aligned workspace of %zu bytes (got %zu)", entry,
+                  need, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  }
   const int64_t tiles_m = (rows + kBM - 1) / kBM;
   const int64_t tiles_n = 3 * d_model / kBN;
 
   LinearParams prm = {};
+  prm.ln_w = ln_weight;
+  prm.ln_b = ln_bias;
+  prm.ln_stats = static_cast<const float2*>(workspace);
   prm.x = x;
   prm.w = weight;
   prm.bias = bias;
@@ -429,6 +584,49 @@ extern "C" int sah_qkv_projection(const void* x, const void* weight, const void*
   prm.v_seq_major = value_layout == SAH_QKV_VALUE_SEQ_MAJOR;
   prm.seq_aligned = seq_len % 8 == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ln) {
+    float2* stats = static_cast<float2*>(workspace);
+    const int status = dtype == SAH_DTYPE_BF16 ? row_stats<bf16>(x, x_row_stride, rows, d_model, ln_eps, stats, s)
+                                               : row_stats<f16>(x, x_row_stride, rows, d_model, ln_eps, stats, s);
+    if (status != SAH_OK) return status;
+    return dtype == SAH_DTYPE_BF16 ? launch_linear<bf16, kEpiHeads, true>(prm, s)
+                                   : launch_linear<f16, kEpiHeads, true>(prm, s);
+  }
   return dtype == SAH_DTYPE_BF16 ? launch_linear<bf16, kEpiHeads>(prm, s)
                                  : launch_linear<f16, kEpiHeads>(prm, s);
+}
+}  // namespace
+
+extern "C" int sah_qkv_projection(const void* x, const void* weight, const void* bias, void* query,
+                                  void* key, void* value, int64_t batch, int64_t seq_len,
+                                  int64_t d_model, int64_t heads, int64_t x_row_stride,
+                                  int value_layout, int64_t value_seq_stride, int dtype,
+                                  int block_m, int block_n, int block_k, int num_warps,
+                                  sah_stream_t stream) {
+  return qkv_projection(x, nullptr, nullptr, 0.0f, weight, bias, query, key, value, batch, seq_len,
+                        d_model, heads, x_row_stride, value_layout, value_seq_stride, dtype, block_m,
+                        block_n, block_k, num_warps, nullptr, 0, stream);
+}
+
+extern "C" size_t sah_norm_qkv_workspace_bytes(int64_t batch, int64_t seq_len) {
+  if (batch <= 0 || seq_len <= 0 || batch > INT64_MAX / 8 / seq_len) return 0;
+  return (size_t)(batch * seq_len) * sizeof(float2);
+}
+
+extern "C" int sah_norm_qkv_projection(const void* x, const void* ln_weight, const void* ln_bias,
+                                       float ln_eps, const void* weight, const void* bias,
+                                       void* query, void* key, void* value, int64_t batch,
+                                       int64_t seq_len, int64_t d_model, int64_t heads,
+                                       int64_t x_row_stride, int value_layout,
+                                       int64_t value_seq_stride, int dtype, int block_m,
+                                       int block_n, int block_k, int num_warps,
+                                       void* workspace, size_t workspace_bytes,
+                                       sah_stream_t stream) {
+  if (ln_weight == nullptr || ln_bias == nullptr)
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "sah_norm_qkv_projection: LayerNorm weight and bias are both required");
+  return qkv_projection(x, ln_weight, ln_bias, ln_eps, weight, bias, query, key, value, batch,
+                        seq_len, d_model, heads, x_row_stride, value_layout, value_seq_stride,
+                        dtype, block_m, block_n, block_k, num_warps, workspace, workspace_bytes,
+                        stream);
 }

@@ -263,7 +263,8 @@ __global__ __launch_bounds__(kLnThreads) void linear_norm_kernel(LinearNormParam
       const int col = (it * 64 + lane) * 8;
       float y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = (v[it * 8 + e] - mean) * rstd * w[it * 8 + e] + b[it * 8 + e];
+      for (int e = 0; e < 8; ++e)
+        y[e] = fp32_result<T>((v[it * 8 + e] - mean) * rstd * w[it * 8 + e] + b[it * 8 + e]);
       store16(yg + base + col, pack8<T>(y));
     }
   }

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(512) void norm_kernel(
     for (int e = 0; e < N; ++e) {
       const float we = has_w ? to_f32(w_raw[e / VEC][e % VEC]) : 1.0f;
       const float be = has_b ? to_f32(b_raw[e / VEC][e % VEC]) : 0.0f;
-      y[e] = (v[e] - mean) * rstd * we + be;
+      y[e] = fp32_result<TY>((v[e] - mean) * rstd * we + be);
     }
 #pragma unroll
     for (int i = 0; i < ITERS; ++i) {

@@ -64,6 +64,18 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return (bf16)x; }
 template <>
 __device__ __forceinline__ f16 from_f32<f16>(float x) { return (f16)x; }
 
+// An fp32 result that a later narrowing to T must round as it stands.  For
+// T = f16 the compiler would otherwise fold "fma in fp32, then round to f16"
+// into v_fma_mix{lo,hi}_f16, which rounds the exact FMA result once and
+// differs from rounding the fp32 result in rare cases; the empty register
+// constraint keeps the two steps apart (no instruction is emitted), so every
+// kernel that rounds a normalized row to f16 rounds it the same way.
+template <typename T>
+__device__ __forceinline__ float fp32_result(float v) {
+  if constexpr (__is_same(T, f16)) asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Round-trip through the storage type (used where the reference rounds an
 // intermediate to the model dtype, e.g. the residual stream).
 template <typename T>
@@ -131,17 +143,31 @@ __device__ __forceinline__ u32x4 pack8(const float* in) {
 
 // Row statistics across a wavefront (the fused norms).
 // Merge Welford states of equal count across the wavefront (butterfly, so
-// every lane ends with the row statistics).
-__device__ __forceinline__ void wave_welford(float& mean, float& m2, float count) {
+// every lane ends with the row statistics), for G independent rows at once:
+// each step's cross-lane exchanges of all G rows are issued together, so
+// their latencies overlap.  Every row is merged exactly as with G = 1.
+template <int G>
+__device__ __forceinline__ void wave_welford_rows(float* mean, float* m2, float count) {
 #pragma unroll
   for (int offset = 1; offset < 64; offset <<= 1) {
-    const float other_mean = __shfl_xor(mean, offset);
-    const float other_m2 = __shfl_xor(m2, offset);
-    const float delta = other_mean - mean;
-    mean = 0.5f * (mean + other_mean);
-    m2 = m2 + other_m2 + delta * delta * (0.5f * count);
+    float other_mean[G], other_m2[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      other_mean[g] = __shfl_xor(mean[g], offset);
+      other_m2[g] = __shfl_xor(m2[g], offset);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float delta = other_mean[g] - mean[g];
+      mean[g] = 0.5f * (mean[g] + other_mean[g]);
+      m2[g] = m2[g] + other_m2[g] + delta * delta * (0.5f * count);
+    }
     count *= 2.0f;
   }
+}
+
+__device__ __forceinline__ void wave_welford(float& mean, float& m2, float count) {
+  wave_welford_rows<1>(&mean, &m2, count);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

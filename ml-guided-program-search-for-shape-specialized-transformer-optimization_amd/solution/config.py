@@ -20,6 +20,9 @@ the schema (version 4) is unchanged:
   rows per workgroup of num_warps wavefronts).
 * ``InitialNormBackend.HIP`` - the layer-0 LayerNorm; launch in
   ``initial_norm_launch``.
+* ``InitialNormBackend.HIP_FUSED_QKV`` - the layer-0 LayerNorm fused into the
+  HIP native-layout QKV projection (the reference's ``TRITON_FUSED_QKV``);
+  like it, no ``initial_norm_launch``: it runs with ``qkv_launch``.
 
 Python 3.10 has no ``enum.StrEnum``; ``str``-mixin enums serialize through
 ``.value`` exactly like the reference's StrEnum members.
@@ -114,6 +117,7 @@ class InitialNormBackend(_StrEnum):
     TRITON_FP16 = "triton_fp16"
     TRITON_FUSED_QKV = "triton_fused_qkv"
     HIP = "hip"
+    HIP_FUSED_QKV = "hip_fused_qkv"
 
 
 class RuntimeBackend(_StrEnum):
@@ -695,6 +699,7 @@ def hip_config(
     qkv: QKVMaterialization = QKVMaterialization.VIEW,
     residual_norm: ResidualNormBackend = ResidualNormBackend.HIP_FUSED,
     boundary_launch: NormLaunchParams | None = None,
+    initial_norm: InitialNormBackend = InitialNormBackend.HIP,
 ) -> ConfigSpec:
     """The gfx950 program for 16-bit models: HIP attention, HIP fused residual
     norms and HIP initial norm, projections in the model dtype on hipBLASLt,
@@ -709,8 +714,9 @@ def hip_config(
     ``residual_norm`` picks the boundary: HIP_FUSED (residual + norm after the
     hipBLASLt output projections, with ``norm_launch``) or HIP_LINEAR_FUSED
     (each output projection fused into its boundary, with ``boundary_launch``,
-    see hip_linear_boundary_launch); the initial norm always uses
-    ``norm_launch``."""
+    see hip_linear_boundary_launch).  ``initial_norm`` picks the layer-0
+    LayerNorm: HIP (its own kernel, with ``norm_launch``) or HIP_FUSED_QKV
+    (fused into the HIP_NATIVE_BHSD projection, which it requires)."""
 
     ffn = FFNBackend(ffn)
     if ffn not in {FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU}:
@@ -718,6 +724,11 @@ def hip_config(
     qkv = QKVMaterialization(qkv)
     if qkv not in {QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD}:
         raise ValueError(f"QKV materialization {qkv.value!r} is not part of the gfx950 program")
+    initial_norm = InitialNormBackend(initial_norm)
+    if initial_norm not in {InitialNormBackend.HIP, InitialNormBackend.HIP_FUSED_QKV}:
+        raise ValueError(f"initial norm {initial_norm.value!r} is not part of the gfx950 program")
+    if initial_norm is InitialNormBackend.HIP_FUSED_QKV and qkv is not QKVMaterialization.HIP_NATIVE_BHSD:
+        raise ValueError("the fused initial norm runs inside the HIP_NATIVE_BHSD QKV projection")
     residual_norm = ResidualNormBackend(residual_norm)
     if residual_norm is ResidualNormBackend.HIP_LINEAR_FUSED:
         if boundary_launch is None:
@@ -748,14 +759,14 @@ def hip_config(
             attention_output_bridge=AttentionOutputBridge.ATTENTION_DIRECT_BSD,
             ffn=ffn,
             residual_norm=residual_norm,
-            initial_norm=InitialNormBackend.HIP,
+            initial_norm=initial_norm,
         ),
         schedule=ScheduleConfig(
             runtime=runtime,
             attention_launch=attention_launch,
             qkv_launch=HIP_QKV_LAUNCH if qkv is QKVMaterialization.HIP_NATIVE_BHSD else None,
             residual_norm_launch=residual_launch,
-            initial_norm_launch=norm_launch,
+            initial_norm_launch=norm_launch if initial_norm is InitialNormBackend.HIP else None,
             ffn_launch=HIP_GELU_LAUNCH if ffn is FFNBackend.HIP_EXACT_GELU else None,
             ffn_input_launch=HIP_LINEAR_LAUNCH if ffn is FFNBackend.HIP_LINEAR_EXACT_GELU else None,
             microbatch_size=microbatch_size,

@@ -87,6 +87,12 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
         [_ptr] * 6 + [_i64] * 5 + [_int, _i64] + [_int] * 5 + [_ptr],
         _int,
     ),
+    "sah_norm_qkv_projection": (
+        [_ptr] * 3 + [ctypes.c_float] + [_ptr] * 5 + [_i64] * 5 + [_int, _i64] + [_int] * 5
+        + [_ptr, ctypes.c_size_t, _ptr],
+        _int,
+    ),
+    "sah_norm_qkv_workspace_bytes": ([_i64, _i64], ctypes.c_size_t),
     "sah_qkv_launch_supported": ([_int] * 4, _int),
     "sah_linear_residual_norm": (
         [_ptr] * 8 + [_i64] * 4 + [ctypes.c_float] + [_int] * 4 + [_ptr],

@@ -21,6 +21,18 @@ transpose pass and no workspace.
 Differences in domain from the reference (fp16, D in {32, 128, 1024},
 S in {32, 128, 1024}, H in {1, 2, 4, 16}): bf16 or fp16, any batch and
 sequence length with B*S < 2^31, D a multiple of 256, head_dim a multiple of 8.
+
+``*_initial_norm_qkv_native_bhsd`` fuse the model's first LayerNorm into the
+projection, the reference's initial-norm / QKV fusion
+(solution/kernels/projection/triton_shape07_initial_norm_qkv.py:67-140, fp32
+statistics, the normalized row rounded to the operand dtype before the dot,
+head-major stores): ``sah_norm_qkv_projection`` forms each row's statistics
+exactly as the fused norm kernel does (into an 8-byte-per-token workspace
+allocated here from torch's caching allocator), and the projection normalizes
+x as it stages it, so the normalized rows never reach HBM and Q / K / V equal,
+bit for bit, those of ``sah_norm`` followed by ``sah_qkv_projection``.  Domain: D in
+{512, 1024, 2048, 4096} (the reference's kernel serves one shape, B64 S128
+D32 H4 fp32, :143-170); the LayerNorm's weight and bias in the operand dtype.
 """
 
 from __future__ import annotations
@@ -39,6 +51,8 @@ from ..hip._library import (
 )
 
 HIP_QKV_NATIVE_BHSD_BACKEND = "hip_qkv_native_bhsd"
+HIP_INITIAL_NORM_QKV_BACKEND = "hip_initial_norm_qkv_native_bhsd"
+INITIAL_NORM_WIDTHS = frozenset({512, 1024, 2048, 4096})
 DEFAULT_BLOCK_M = 256
 DEFAULT_BLOCK_N = 256
 DEFAULT_BLOCK_K = 64
@@ -130,6 +144,60 @@ def can_use_hip_qkv_native_bhsd(
     return is_gfx950(hidden_states.device)
 
 
+def _layer_norm_parameters(layer_norm: torch.nn.LayerNorm) -> tuple[torch.Tensor, torch.Tensor, float] | None:
+    weight, bias = layer_norm.weight, layer_norm.bias
+    if not isinstance(weight, torch.Tensor) or not isinstance(bias, torch.Tensor):
+        return None
+    return weight, bias, float(layer_norm.eps)
+
+
+def can_use_hip_initial_norm_qkv_native_bhsd(
+    hidden_states: torch.Tensor,
+    layer_norm: torch.nn.LayerNorm,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    num_heads: int,
+    block_m: int = DEFAULT_BLOCK_M,
+    block_n: int = DEFAULT_BLOCK_N,
+    block_k: int = DEFAULT_BLOCK_K,
+    num_warps: int = DEFAULT_NUM_WARPS,
+) -> bool:
+    """The projection's rules plus the LayerNorm's: an affine LayerNorm over
+    the last dimension of a width the statistics are instantiated for, its
+    weight and bias contiguous and in the operand dtype, a finite eps >= 0.
+    Never raises."""
+
+    if not isinstance(layer_norm, torch.nn.LayerNorm):
+        return False
+    parameters = _layer_norm_parameters(layer_norm)
+    if parameters is None:
+        return False
+    norm_weight, norm_bias, eps = parameters
+    if not isinstance(hidden_states, torch.Tensor) or hidden_states.ndim != 3:
+        return False
+    d_model = hidden_states.shape[-1]
+    if tuple(layer_norm.normalized_shape) != (d_model,) or d_model not in INITIAL_NORM_WIDTHS:
+        return False
+    if not (eps >= 0.0 and eps < float("inf")):
+        return False
+    for tensor in (norm_weight, norm_bias):
+        if tensor.shape != (d_model,) or tensor.dtype != hidden_states.dtype:
+            return False
+        if tensor.device != hidden_states.device or not tensor.is_contiguous() or tensor.data_ptr() % 16:
+            return False
+    return can_use_hip_qkv_native_bhsd(
+        hidden_states,
+        weight,
+        bias,
+        num_heads=num_heads,
+        block_m=block_m,
+        block_n=block_n,
+        block_k=block_k,
+        num_warps=num_warps,
+    )
+
+
 def prevalidated_hip_qkv_native_bhsd(
     hidden_states: torch.Tensor,
     weight: torch.Tensor,
@@ -163,6 +231,64 @@ def prevalidated_hip_qkv_native_bhsd(
         num_warps=num_warps,
     ):
         raise RuntimeError("HIP QKV native-layout projection inputs are ineligible for the gfx950 kernel")
+    return _launch(
+        hidden_states, None, weight, bias, num_heads, (block_m, block_n, block_k, num_warps), value_layout
+    ) + (HIP_QKV_NATIVE_BHSD_BACKEND,)
+
+
+def prevalidated_hip_initial_norm_qkv_native_bhsd(
+    hidden_states: torch.Tensor,
+    layer_norm: torch.nn.LayerNorm,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    num_heads: int,
+    block_m: int = DEFAULT_BLOCK_M,
+    block_n: int = DEFAULT_BLOCK_N,
+    block_k: int = DEFAULT_BLOCK_K,
+    num_warps: int = DEFAULT_NUM_WARPS,
+    value_layout: str = "bhsd",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, str]:
+    """``layer_norm(hidden_states)`` projected into head-major Q / K / V in
+    one kernel; the normalized rows never reach HBM (reference: the fused
+    initial-norm QKV launch, triton_shape07_initial_norm_qkv.py:173-218).
+    Same return value and errors as :func:`prevalidated_hip_qkv_native_bhsd`."""
+
+    _validate_launch_config(block_m, block_n, block_k, num_warps)
+    if value_layout not in VALUE_LAYOUTS:
+        raise ValueError(f"unknown value layout {value_layout!r}; expected one of {sorted(VALUE_LAYOUTS)}")
+    if not can_use_hip_initial_norm_qkv_native_bhsd(
+        hidden_states,
+        layer_norm,
+        weight,
+        bias,
+        num_heads=num_heads,
+        block_m=block_m,
+        block_n=block_n,
+        block_k=block_k,
+        num_warps=num_warps,
+    ):
+        raise RuntimeError("HIP initial-norm QKV projection inputs are ineligible for the gfx950 kernel")
+    return _launch(
+        hidden_states,
+        _layer_norm_parameters(layer_norm),
+        weight,
+        bias,
+        num_heads,
+        (block_m, block_n, block_k, num_warps),
+        value_layout,
+    ) + (HIP_INITIAL_NORM_QKV_BACKEND,)
+
+
+def _launch(
+    hidden_states: torch.Tensor,
+    layer_norm: tuple[torch.Tensor, torch.Tensor, float] | None,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    num_heads: int,
+    launch: tuple[int, int, int, int],
+    value_layout: str,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     batch, seq_len, d_model = hidden_states.shape
     head_dim = d_model // num_heads
     shape = (batch, num_heads, seq_len, head_dim)
@@ -176,32 +302,46 @@ def prevalidated_hip_qkv_native_bhsd(
     else:
         seq_stride = 0
         value = torch.empty_like(query)
+    operands = (
+        weight.data_ptr(),
+        None if bias is None else bias.data_ptr(),
+        query.data_ptr(),
+        key.data_ptr(),
+        value.data_ptr(),
+        batch,
+        seq_len,
+        d_model,
+        num_heads,
+        hidden_states.stride(1),
+        VALUE_LAYOUTS[value_layout],
+        seq_stride,
+        dtype_code(dtype),
+        *launch,
+        stream_handle(device),
+    )
+    library = load_library()
     try:
-        status = load_library().sah_qkv_projection(
-            hidden_states.data_ptr(),
-            weight.data_ptr(),
-            None if bias is None else bias.data_ptr(),
-            query.data_ptr(),
-            key.data_ptr(),
-            value.data_ptr(),
-            batch,
-            seq_len,
-            d_model,
-            num_heads,
-            hidden_states.stride(1),
-            VALUE_LAYOUTS[value_layout],
-            seq_stride,
-            dtype_code(dtype),
-            block_m,
-            block_n,
-            block_k,
-            num_warps,
-            stream_handle(device),
-        )
-        check_status(status, "sah_qkv_projection")
+        if layer_norm is None:
+            status = library.sah_qkv_projection(hidden_states.data_ptr(), *operands)
+            check_status(status, "sah_qkv_projection")
+        else:
+            norm_weight, norm_bias, eps = layer_norm
+            workspace_bytes = int(library.sah_norm_qkv_workspace_bytes(batch, seq_len))
+            workspace = torch.empty(max(workspace_bytes, 16), device=device, dtype=torch.uint8)
+            status = library.sah_norm_qkv_projection(
+                hidden_states.data_ptr(),
+                norm_weight.data_ptr(),
+                norm_bias.data_ptr(),
+                eps,
+                *operands[:-1],
+                workspace.data_ptr(),
+                workspace.numel(),
+                operands[-1],
+            )
+            check_status(status, "sah_norm_qkv_projection")
     except Exception as exc:
         raise RuntimeError("HIP QKV native-layout projection execution failed") from exc
-    return query, key, value, HIP_QKV_NATIVE_BHSD_BACKEND
+    return query, key, value
 
 
 def hip_qkv_native_bhsd(
@@ -249,12 +389,16 @@ __all__ = [
     "DEFAULT_BLOCK_M",
     "DEFAULT_BLOCK_N",
     "DEFAULT_NUM_WARPS",
+    "HIP_INITIAL_NORM_QKV_BACKEND",
     "HIP_QKV_NATIVE_BHSD_BACKEND",
+    "INITIAL_NORM_WIDTHS",
     "VALUE_LAYOUTS",
+    "can_use_hip_initial_norm_qkv_native_bhsd",
     "can_use_hip_qkv_native_bhsd",
     "hip_qkv_native_bhsd",
     "hip_qkv_native_bhsd_available",
     "launch_config_is_valid",
+    "prevalidated_hip_initial_norm_qkv_native_bhsd",
     "prevalidated_hip_qkv_native_bhsd",
     "supported_shape",
 ]

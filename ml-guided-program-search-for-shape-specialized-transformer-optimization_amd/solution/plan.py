@@ -214,6 +214,13 @@ class ExecutionPlan:
         return self.initial_norm_backend is InitialNormBackend.HIP
 
     @property
+    def use_fused_initial_norm_qkv(self) -> bool:
+        """Layer 0's LayerNorm runs inside its QKV projection (reference
+        :255-256)."""
+
+        return self.initial_norm_backend is InitialNormBackend.HIP_FUSED_QKV
+
+    @property
     def use_hip_residual_norm(self) -> bool:
         return self.residual_norm_backend in {
             ResidualNormBackend.HIP_FUSED,

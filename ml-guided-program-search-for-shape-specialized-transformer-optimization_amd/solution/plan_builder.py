@@ -661,6 +661,9 @@ class PlanBuilder:
         backend = config.program.initial_norm
         if backend is InitialNormBackend.TORCH:
             return
+        if backend is InitialNormBackend.HIP_FUSED_QKV:
+            PlanBuilder._validate_fused_initial_norm_qkv(config, context, hardware, reject)
+            return
         if backend is not InitialNormBackend.HIP:
             _unavailable(reject, "program.initial_norm", f"Triton initial norm {backend.value}")
             return
@@ -680,6 +683,44 @@ class PlanBuilder:
             reject("unsupported_dtype", field, "HIP initial norm supports FP32, FP16 and BF16 inputs")
         elif not supported_width(context.d_model, context.dtype):
             reject("unsupported_shape", field, "HIP initial norm has no kernel for this width")
+
+    @staticmethod
+    def _validate_fused_initial_norm_qkv(
+        config: ConfigSpec,
+        context: ExecutionContext,
+        hardware: HardwareCapabilities,
+        reject: Reject,
+    ) -> None:
+        """The reference's TRITON_FUSED_QKV rules (solution/plan_builder.py:
+        1100-1159) for the gfx950 kernel: no launch of its own, the
+        native-layout QKV projection, no mask; its own shape domain (16-bit
+        models of width 512-4096) instead of the reference's one fp32 shape,
+        and any runtime."""
+
+        from .kernels.projection.hip_qkv_layout import INITIAL_NORM_WIDTHS
+
+        field = "program.initial_norm"
+        if config.schedule.initial_norm_launch is not None:
+            reject(
+                "launch_incompatible",
+                "schedule.initial_norm_launch",
+                "the fused initial norm uses the QKV launch configuration",
+            )
+        _validate_hip_common(context, hardware, hardware.hip_qkv_native_bhsd, field, reject)
+        if config.program.qkv_materialization is not QKVMaterialization.HIP_NATIVE_BHSD:
+            reject(
+                "qkv_incompatible",
+                field,
+                "the fused initial norm requires the HIP native-layout QKV projection",
+            )
+        if context.dtype not in {torch.float16, torch.bfloat16}:
+            reject("unsupported_dtype", field, "the fused initial norm runs on FP16 and BF16 models")
+        if context.d_model not in INITIAL_NORM_WIDTHS:
+            reject(
+                "unsupported_shape",
+                field,
+                "the fused initial norm supports d_model 512, 1024, 2048 and 4096",
+            )
 
     # -------------------------------------------------------------------- build
     @staticmethod

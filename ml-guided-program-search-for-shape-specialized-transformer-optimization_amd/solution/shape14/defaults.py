@@ -66,6 +66,7 @@ def hip_streamed_config(
     qkv: QKVMaterialization = QKVMaterialization.VIEW,
     residual_norm: ResidualNormBackend = ResidualNormBackend.HIP_FUSED,
     boundary_launch: NormLaunchParams | None = None,
+    initial_norm: InitialNormBackend = InitialNormBackend.HIP,
 ) -> ConfigSpec:
     """The gfx950 long-sequence program with ordered microbatches."""
 
@@ -76,6 +77,7 @@ def hip_streamed_config(
         qkv=qkv,
         residual_norm=residual_norm,
         boundary_launch=boundary_launch,
+        initial_norm=initial_norm,
     )
 
 

@@ -304,29 +304,34 @@ class _SelfAttention(nn.Module):
         observation: _ExecutionObservation | None,
         *,
         project: bool = True,
+        initial_norm: nn.LayerNorm | None = None,
     ) -> torch.Tensor:
         """The attention branch.  With ``project=False`` (the linear-boundary
         plans, reference :620-726) it returns the [B, S, D] context before the
-        output projection, which the fused boundary multiplies."""
+        output projection, which the fused boundary multiplies.  With
+        ``initial_norm`` (layer 0 of a fused initial-norm plan, reference
+        :1419-1423) ``value`` is the un-normalized input and the LayerNorm runs
+        inside the QKV projection."""
 
         batch, seq, _ = value.shape
         backend = plan.attention_backend
+        if initial_norm is not None and plan.qkv_materialization is not QKVMaterialization.HIP_NATIVE_BHSD:
+            raise RuntimeError("the fused initial norm needs the HIP native-layout QKV projection")
         if plan.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD:
             # The reference's native-layout branch (solution/transformer.py:384-431):
             # the projection kernel writes head-major Q / K / V itself.  The HIP
             # attention reads V^T, so V is written seq-contiguous for it.
             from .kernels.projection.hip_qkv_layout import (
+                HIP_INITIAL_NORM_QKV_BACKEND,
                 HIP_QKV_NATIVE_BHSD_BACKEND,
+                prevalidated_hip_initial_norm_qkv_native_bhsd,
                 prevalidated_hip_qkv_native_bhsd,
             )
 
             launch = plan.qkv_launch
             if launch is None:
                 raise RuntimeError("HIP native-layout QKV plan is missing launch parameters")
-            query, key, projected, marker = prevalidated_hip_qkv_native_bhsd(
-                value,
-                self.qkv_proj.weight,
-                self.qkv_proj.bias,
+            launch_args = dict(
                 num_heads=self.num_heads,
                 block_m=launch.block_m,
                 block_n=launch.block_n,
@@ -334,9 +339,19 @@ class _SelfAttention(nn.Module):
                 num_warps=launch.num_warps,
                 value_layout="seq_major" if backend is AttentionBackend.HIP_STREAMING_DH64 else "bhsd",
             )
+            if initial_norm is None:
+                query, key, projected, marker = prevalidated_hip_qkv_native_bhsd(
+                    value, self.qkv_proj.weight, self.qkv_proj.bias, **launch_args
+                )
+                expected = HIP_QKV_NATIVE_BHSD_BACKEND
+            else:
+                query, key, projected, marker = prevalidated_hip_initial_norm_qkv_native_bhsd(
+                    value, initial_norm, self.qkv_proj.weight, self.qkv_proj.bias, **launch_args
+                )
+                expected = HIP_INITIAL_NORM_QKV_BACKEND
             _strict_backend_marker(
                 marker,
-                expected_marker=HIP_QKV_NATIVE_BHSD_BACKEND,
+                expected_marker=expected,
                 planned_backend=plan.qkv_materialization.value,
             )
             qkv_dtype = query.dtype
@@ -459,8 +474,11 @@ class _TransformerBlock(nn.Module):
         observation: _ExecutionObservation | None,
         *,
         project: bool = True,
+        initial_norm: nn.LayerNorm | None = None,
     ) -> torch.Tensor:
-        return self.attention(normalized, valid_token_mask, causal, plan, observation, project=project)
+        return self.attention(
+            normalized, valid_token_mask, causal, plan, observation, project=project, initial_norm=initial_norm
+        )
 
     def ffn_update(
         self,
@@ -807,7 +825,10 @@ class UserOptimizedTransformer(nn.Module):
     ) -> torch.Tensor:
         norm = self.layers[0].norm1
         branch_dtype = torch.float16 if plan.use_mixed_residual_stream else value.dtype
-        if plan.initial_norm_backend is InitialNormBackend.HIP:
+        if plan.use_fused_initial_norm_qkv:
+            # layer 0's QKV projection normalizes (reference :1364-1371)
+            normalized = value
+        elif plan.initial_norm_backend is InitialNormBackend.HIP:
             from .kernels.norm.hip_residual import HIP_LAYER_NORM_BACKEND, hip_layer_norm
 
             launch = plan.initial_norm_launch
@@ -867,9 +888,10 @@ class UserOptimizedTransformer(nn.Module):
                 observation.layer_input_dtypes.append(_dtype_name(value.dtype))
             last = index + 1 == len(self.layers)
             next_norm = self.final_norm if last else self.layers[index + 1].norm1
+            initial_norm = layer.norm1 if index == 0 and plan.use_fused_initial_norm_qkv else None
             if fused:
                 context = layer.attention_update(
-                    normalized, valid_token_mask, causal, plan, observation, project=False
+                    normalized, valid_token_mask, causal, plan, observation, project=False, initial_norm=initial_norm
                 )
                 value, normalized = self._apply_linear_boundary(
                     context, layer.attention.out_proj, value, layer.norm2, plan, observation
@@ -879,7 +901,9 @@ class UserOptimizedTransformer(nn.Module):
                     hidden, layer.ffn_out, value, next_norm, plan, observation, out=out if last else None
                 )
             else:
-                update = layer.attention_update(normalized, valid_token_mask, causal, plan, observation)
+                update = layer.attention_update(
+                    normalized, valid_token_mask, causal, plan, observation, initial_norm=initial_norm
+                )
                 value, normalized = self._apply_residual_norm(
                     value, update, layer.norm2, valid_token_mask, plan, observation, final_boundary=False
                 )

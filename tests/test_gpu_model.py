@@ -243,14 +243,16 @@ def test_hip_programs_on_an_fp16_model_match_the_fp16_reference_path(gpu_device,
 
 
 def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
-    """The graph-replay runtime with every fused GEMM epilogue (native-layout
-    QKV, Linear + exact GELU, the Linear + residual + LayerNorm boundaries):
+    """The graph-replay runtime with every fused GEMM epilogue and prologue
+    (the initial LayerNorm fused into the native-layout QKV projection,
+    Linear + exact GELU, the Linear + residual + LayerNorm boundaries):
     several replays with new inputs, eager work
     and synchronizations between them, each bitwise equal to the eager
     program on the same input."""
 
     from solution.config import (
         FFNBackend,
+        InitialNormBackend,
         QKVMaterialization,
         ResidualNormBackend,
         hip_config,
@@ -264,6 +266,7 @@ def test_graph_runtime_replays_the_fused_projection_programs(gpu_device):
         qkv=QKVMaterialization.HIP_NATIVE_BHSD,
         residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED,
         boundary_launch=hip_linear_boundary_launch(512),
+        initial_norm=InitialNormBackend.HIP_FUSED_QKV,
     )
     graph_model = _model(config, state, gpu_device, torch.bfloat16)
     graph_model.configure_execution(config=hip_config(graph=True, **options))

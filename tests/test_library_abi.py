@@ -199,3 +199,42 @@ def test_qkv_projection_entry_validates_before_launch():
     assert call(layout=_library.SAH_QKV_VALUE_BHSD, ldv=0, batch=0) == _library.SAH_OK
     status = call(x=ctypes.c_void_p(4096 + 8))
     assert status == _library.SAH_ERR_INVALID_ARGUMENT and b"aligned" in library.sah_last_error()
+
+
+def test_norm_qkv_projection_entry_validates_before_launch():
+    """sah_norm_qkv_projection: the projection's checks (reported under its
+    own name) plus the LayerNorm's, all before any kernel runs."""
+
+    library = _library.load_library()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    base = dict(batch=2, seq=100, d=1024, heads=16, ldx=1024, layout=_library.SAH_QKV_VALUE_SEQ_MAJOR,
+                ldv=104, dtype=2, launch=(256, 256, 64, 8), ln_w=fake, ln_b=fake, eps=1e-5, ws=fake, ws_bytes=1600)
+
+    def call(**over):
+        a = {**base, **over}
+        return library.sah_norm_qkv_projection(fake, a["ln_w"], a["ln_b"], a["eps"], fake, None, fake, fake, fake,
+                                               a["batch"], a["seq"], a["d"], a["heads"], a["ldx"], a["layout"],
+                                               a["ldv"], a["dtype"], *a["launch"], a["ws"], a["ws_bytes"], None)
+
+    assert call(ln_b=None) == _library.SAH_ERR_INVALID_ARGUMENT and b"both required" in library.sah_last_error()
+    assert call(ln_w=None, ln_b=None) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ln_w=ctypes.c_void_p(4096 + 8)) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(eps=float("nan")) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(eps=-1e-5) == _library.SAH_ERR_INVALID_ARGUMENT
+    # widths with statistics instantiated: 512, 1024, 2048, 4096
+    assert call(d=768, heads=12, ldx=768) == _library.SAH_ERR_UNSUPPORTED
+    assert b"512, 1024, 2048 or 4096" in library.sah_last_error()
+    assert call(d=8192, heads=128, ldx=8192) == _library.SAH_ERR_UNSUPPORTED
+    # the projection's own checks, named for this entry point
+    assert call(launch=(64, 32, 32, 4)) == _library.SAH_ERR_UNSUPPORTED
+    assert library.sah_last_error().startswith(b"sah_norm_qkv_projection:")
+    assert call(ldx=1000) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(batch=0) == _library.SAH_OK
+    assert call(batch=0, ln_b=None) == _library.SAH_ERR_INVALID_ARGUMENT  # checked even with nothing to do
+    # the statistics workspace: 8 bytes per token, 16-byte aligned
+    assert library.sah_norm_qkv_workspace_bytes(2, 100) == 1600
+    assert library.sah_norm_qkv_workspace_bytes(0, 100) == 0 and library.sah_norm_qkv_workspace_bytes(2, -1) == 0
+    assert library.sah_norm_qkv_workspace_bytes(2**40, 2**30) == 0  # no overflow
+    assert call(ws_bytes=1599) == _library.SAH_ERR_WORKSPACE and b"1600" in library.sah_last_error()
+    assert call(ws=None) == _library.SAH_ERR_WORKSPACE
+    assert call(ws=ctypes.c_void_p(4096 + 8)) == _library.SAH_ERR_WORKSPACE

@@ -475,6 +475,65 @@ def test_native_qkv_plans_and_rejections():
     assert ("program.qkv_materialization", "backend_unavailable") in codes(builder.evaluate(triton, _context(), _gfx950()))
 
 
+def test_fused_initial_norm_qkv_plans_and_rejections():
+    """Layer 0's LayerNorm inside the HIP native-layout QKV projection: no
+    launch of its own, the native projection required, 16-bit widths
+    512-4096, no mask (the reference's TRITON_FUSED_QKV rules,
+    solution/plan_builder.py:1100-1159, with this kernel's domain)."""
+
+    from solution.config import HIP_DEFAULT_NORM_LAUNCH, QKVMaterialization
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    fused = hip_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD, initial_norm=InitialNormBackend.HIP_FUSED_QKV)
+    assert fused.program.initial_norm is InitialNormBackend.HIP_FUSED_QKV
+    assert fused.schedule.initial_norm_launch is None
+    assert ConfigSpec.from_dict(fused.to_dict()) == fused
+    assert fused.to_dict()["program"]["initial_norm"] == "hip_fused_qkv"
+    assert fused.config_id != hip_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD).config_id
+    c2 = _context(batch=64, seq=256, d=512, heads=8, ffn=2048, layers=4)
+    plan = builder.build(fused, c2, _gfx950())
+    assert plan.use_fused_initial_norm_qkv and not plan.use_hip_initial_norm
+    trace = plan.expected_trace.to_dict()
+    assert trace["initial_norm_backend"] == "hip_fused_qkv" and trace["initial_norm_launch"] is None
+    streamed = builder.build(
+        hip_streamed_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD, initial_norm=InitialNormBackend.HIP_FUSED_QKV),
+        _context(),
+        _gfx950(),
+    )
+    assert streamed.use_streamed_execution and streamed.use_fused_initial_norm_qkv
+    # presence rule: no initial_norm_launch for the fused backend
+    with pytest.raises(ValueError, match="initial_norm_launch"):
+        dataclasses.replace(fused, schedule=dataclasses.replace(fused.schedule, initial_norm_launch=HIP_DEFAULT_NORM_LAUNCH))
+    with pytest.raises(ValueError, match="HIP_NATIVE_BHSD"):
+        hip_config(initial_norm=InitialNormBackend.HIP_FUSED_QKV)
+    with pytest.raises(ValueError, match="not part of the gfx950 program"):
+        hip_config(qkv=QKVMaterialization.HIP_NATIVE_BHSD, initial_norm=InitialNormBackend.TRITON_FUSED_QKV)
+    # the native projection is required (a hand-edited program without it)
+    viewed = dataclasses.replace(
+        fused,
+        program=dataclasses.replace(fused.program, qkv_materialization=QKVMaterialization.VIEW),
+        schedule=dataclasses.replace(fused.schedule, qkv_launch=None),
+    )
+    assert ("program.initial_norm", "qkv_incompatible") in codes(builder.evaluate(viewed, c2, _gfx950()))
+    odd_width = builder.evaluate(fused, _context(d=768, heads=12, ffn=3072), _gfx950())
+    assert ("program.initial_norm", "unsupported_shape") in codes(odd_width)
+    assert ("program.qkv_materialization", "unsupported_shape") not in codes(odd_width)
+    fp32 = builder.evaluate(fused, _context(dtype=torch.float32), _gfx950())
+    assert ("program.initial_norm", "unsupported_dtype") in codes(fp32)
+    masked = builder.evaluate(fused, _context(mask=True), _gfx950())
+    assert ("program.initial_norm", "mask_not_supported") in codes(masked)
+    unavailable = builder.evaluate(fused, c2, _gfx950(hip_qkv_native_bhsd=False))
+    assert ("program.initial_norm", "backend_unavailable") in codes(unavailable)
+    cpu = builder.evaluate(fused, _context(device="cpu"), _gfx950())
+    assert ("program.initial_norm", "requires_gfx950") in codes(cpu)
+    # the reference's Triton fusion stays unavailable, not replaced
+    triton = dataclasses.replace(
+        fused, program=dataclasses.replace(fused.program, initial_norm=InitialNormBackend.TRITON_FUSED_QKV)
+    )
+    assert ("program.initial_norm", "backend_unavailable") in codes(builder.evaluate(triton, c2, _gfx950()))
+
+
 def test_linear_boundary_plans_and_rejections():
     """The HIP Linear + residual + LayerNorm boundary: accepted for 16-bit
     inference on gfx950 at widths 512 and 1024 with its launch, rejected with
