@@ -17,8 +17,9 @@ build:
   activation path (hipBLASLt + torch GELU, hipBLASLt + the HIP elementwise
   GELU, or the fused HIP Linear + exact-GELU kernel where the plan builder
   accepts it), then the QKV path (hipBLASLt packed projection with zero-copy
-  views, or the HIP projection writing head-major Q / K and the attention's
-  V^T layout), then the residual boundary (hipBLASLt output projections
+  views, the HIP projection writing head-major Q / K and the attention's
+  V^T layout, or that projection with the initial LayerNorm fused in), then
+  the residual boundary (hipBLASLt output projections
   followed by the HIP residual norm, or the fused HIP Linear + residual +
   LayerNorm boundary where the plan builder accepts it), then runtime, each
   stage keeping the best of the previous ones; a stage replaces the
@@ -66,6 +67,7 @@ from solution.config import (
     AttentionLaunchParams,
     ConfigSpec,
     FFNBackend,
+    InitialNormBackend,
     NormLaunchParams,
     QKVMaterialization,
     ResidualNormBackend,
@@ -160,8 +162,10 @@ def _ffn_variants(config: ConfigSpec) -> list[ConfigSpec]:
 
 
 def _qkv_variants(config: ConfigSpec) -> list[ConfigSpec]:
-    """The QKV paths: hipBLASLt's packed projection viewed as Q / K / V, or
-    the HIP projection with the head-major epilogue, each with its launch."""
+    """The QKV paths: hipBLASLt's packed projection viewed as Q / K / V, the
+    HIP projection with the head-major epilogue, each with its launch, and
+    that projection with layer 0's LayerNorm fused into it (no launch of the
+    initial norm's own)."""
 
     def with_qkv(materialization: QKVMaterialization, launch=None) -> ConfigSpec:
         return dataclasses.replace(
@@ -170,10 +174,13 @@ def _qkv_variants(config: ConfigSpec) -> list[ConfigSpec]:
             schedule=dataclasses.replace(config.schedule, qkv_launch=launch),
         )
 
-    return [
-        with_qkv(QKVMaterialization.VIEW),
-        with_qkv(QKVMaterialization.HIP_NATIVE_BHSD, HIP_QKV_LAUNCH),
-    ]
+    native = with_qkv(QKVMaterialization.HIP_NATIVE_BHSD, HIP_QKV_LAUNCH)
+    fused_initial_norm = dataclasses.replace(
+        native,
+        program=dataclasses.replace(native.program, initial_norm=InitialNormBackend.HIP_FUSED_QKV),
+        schedule=dataclasses.replace(native.schedule, initial_norm_launch=None),
+    )
+    return [with_qkv(QKVMaterialization.VIEW), native, fused_initial_norm]
 
 
 def _boundary_variants(config: ConfigSpec, d_model: int) -> list[ConfigSpec]:
@@ -279,7 +286,7 @@ class HipLaunchSearch:
             self.log(
                 f"{config.config_id[:16]} attention {launch.to_dict() if launch else None} "
                 f"norm {config.schedule.residual_norm_launch.to_dict()} ffn {config.program.ffn.value} "
-                f"qkv {config.program.qkv_materialization.value} "
+                f"qkv {config.program.qkv_materialization.value} initial norm {config.program.initial_norm.value} "
                 f"boundary {config.program.residual_norm.value} runtime "
                 f"{config.schedule.runtime.value}/{config.schedule.microbatch_size}: {ms:.5g} ms/sequence"
             )

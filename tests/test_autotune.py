@@ -148,8 +148,8 @@ def test_ffn_stage_offers_hipblaslt_and_the_fused_kernel():
     assert not no_kernel.legal(variants[1], device) and not no_kernel.legal(variants[2], device)
 
 
-def test_qkv_stage_offers_views_and_the_native_layout_kernel():
-    from solution.config import HIP_QKV_LAUNCH, QKVMaterialization
+def test_qkv_stage_offers_views_the_native_layout_kernel_and_the_fused_initial_norm():
+    from solution.config import HIP_QKV_LAUNCH, InitialNormBackend, QKVMaterialization
 
     for workload in ("c2", "c4", "c5"):
         shape = SearchShape(*WORKLOADS[workload])
@@ -157,15 +157,20 @@ def test_qkv_stage_offers_views_and_the_native_layout_kernel():
         base = search.incumbent()
         variants = _qkv_variants(base)
         assert [v.program.qkv_materialization for v in variants] == [
-            QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD,
+            QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD, QKVMaterialization.HIP_NATIVE_BHSD,
+        ]
+        assert [v.program.initial_norm for v in variants] == [
+            InitialNormBackend.HIP, InitialNormBackend.HIP, InitialNormBackend.HIP_FUSED_QKV,
         ]
         assert variants[0] == base  # the default program is one of them
-        assert variants[1].schedule.qkv_launch == HIP_QKV_LAUNCH
+        assert variants[1].schedule.qkv_launch == variants[2].schedule.qkv_launch == HIP_QKV_LAUNCH
+        assert variants[2].schedule.initial_norm_launch is None
         device = torch.device("cuda")
         assert all(search.legal(v, device) for v in variants), workload
-    # without the kernel the native variant is rejected, never timed
+    # without the kernel the native variants are rejected, never timed
     no_kernel = HipLaunchSearch(torch.nn.Identity(), shape, hardware=_gfx950(hip_qkv_native_bhsd=False))
-    assert no_kernel.legal(variants[0], device) and not no_kernel.legal(variants[1], device)
+    assert no_kernel.legal(variants[0], device)
+    assert not no_kernel.legal(variants[1], device) and not no_kernel.legal(variants[2], device)
 
 
 def test_boundary_stage_offers_the_fused_linear_boundary_where_it_exists():
