@@ -152,8 +152,9 @@ int sah_causal_attention_launch_supported(int block_m, int block_n, int num_warp
  *   (bf16,bf16,bf16) (f16,f16,f16) (f32,f32,f32)
  *   (f32,f16,f16) (f32,f16,f32) (f32,bf16,bf16) (f32,bf16,f32)
  * weight/bias: param_dtype (f32 or the value dtype); either may be NULL
- * (weight 1, bias 0).  width: 512 x {1, 2, 4, 8, 16} for 16-bit value dtypes,
- * 256 x {1, 2, 4, 8, 16} for f32.  Rows are contiguous (row stride == width).
+ * (weight 1, bias 0).  width: 128, 256 or 512 x {1, 2, 4, 8, 16} for 16-bit
+ * value dtypes, 128 or 256 x {1, 2, 4, 8, 16} for f32.  Rows are contiguous
+ * (row stride == width).
  * block_rows rows per workgroup of num_warps wavefronts; block_rows must be a
  * multiple of num_warps; num_warps in {1, 2, 4, 8}.
  */

@@ -9,6 +9,8 @@
 //
 // Mapping: one wavefront per row, 16 bytes per lane per access, so a wave
 // reads 1 KiB per load instruction with every lane's address contiguous.
+// Rows narrower than one such pass (16-bit widths 128 and 256, fp32 width
+// 128) use 4- or 8-byte accesses: VEC = width / 64 elements per lane.
 // Each lane keeps its slice of the row in registers; statistics are a per-lane
 // Welford state (count, mean, M2) merged across the 64 lanes with the
 // pairwise (Chan et al.) update, so HBM is read exactly once per tensor.
@@ -48,13 +50,13 @@ struct VecIO {
 // ONE_ROW: rows_per_wave == 1, compiled as straight-line code, so the affine
 // parameters stay packed until they are used (55 instead of 77 VGPRs at width
 // 1024 bf16: 8 instead of 6 waves per SIMD, 26.6 -> 25.6 us for 16384 rows).
-template <typename TX, typename TU, typename TY, typename TP, int ITERS, bool HAS_RES, bool ONE_ROW>
+template <typename TX, typename TU, typename TY, typename TP, int ITERS, bool HAS_RES, bool ONE_ROW,
+          int VEC = 16 / sizeof(TX)>
 __global__ __launch_bounds__(512) void norm_kernel(
     const TX* __restrict__ value, const TU* __restrict__ update,
     const TP* __restrict__ weight, const TP* __restrict__ bias,
     TX* __restrict__ residual, TY* __restrict__ normalized, int64_t rows,
     float eps, int rows_per_wave, int rms) {
-  constexpr int VEC = 16 / sizeof(TX);
   constexpr int WIDTH = ITERS * kWave * VEC;
   constexpr int N = ITERS * VEC;
   const int lane = threadIdx.x & (kWave - 1);
@@ -168,13 +170,37 @@ struct NormArgs {
   hipStream_t stream;
 };
 
+template <typename TX, typename TU, typename TY, typename TP, bool HAS_RES, int NARROW>
+int launch_narrow(const NormArgs& a) {
+  const int rows_per_wave = a.block_rows / a.num_warps;
+  const int64_t grid = ceil_div(a.rows, a.block_rows);
+  if (grid > INT32_MAX) return fail(SAH_ERR_UNSUPPORTED, "too many rows");
+  const dim3 block(a.num_warps * kWave);
+  if (rows_per_wave == 1)
+    hipLaunchKernelGGL((norm_kernel<TX, TU, TY, TP, 1, HAS_RES, true, NARROW>), dim3(grid), block, 0,
+                       a.stream, static_cast<const TX*>(a.value), static_cast<const TU*>(a.update),
+                       static_cast<const TP*>(a.weight), static_cast<const TP*>(a.bias),
+                       static_cast<TX*>(a.residual), static_cast<TY*>(a.normalized), a.rows, a.eps,
+                       rows_per_wave, a.norm_kind);
+  else
+    hipLaunchKernelGGL((norm_kernel<TX, TU, TY, TP, 1, HAS_RES, false, NARROW>), dim3(grid), block, 0,
+                       a.stream, static_cast<const TX*>(a.value), static_cast<const TU*>(a.update),
+                       static_cast<const TP*>(a.weight), static_cast<const TP*>(a.bias),
+                       static_cast<TX*>(a.residual), static_cast<TY*>(a.normalized), a.rows, a.eps,
+                       rows_per_wave, a.norm_kind);
+  return check_hip(hipGetLastError(), "norm kernel launch");
+}
+
 template <typename TX, typename TU, typename TY, typename TP, bool HAS_RES>
 int launch_typed(const NormArgs& a) {
   constexpr int VEC = 16 / sizeof(TX);
   const int64_t per_iter = (int64_t)kWave * VEC;
+  // Narrow rows: one access of width / 64 elements per lane.
+  if (a.width == 128) return launch_narrow<TX, TU, TY, TP, HAS_RES, 2>(a);
+  if (a.width == 256 && VEC == 8) return launch_narrow<TX, TU, TY, TP, HAS_RES, 4>(a);
   if (a.width % per_iter != 0) {
-    return fail(SAH_ERR_UNSUPPORTED, "norm width %lld is not a multiple of %lld",
-                (long long)a.width, (long long)per_iter);
+    return fail(SAH_ERR_UNSUPPORTED, "norm width %lld is 128, %sor a multiple of %lld",
+                (long long)a.width, VEC == 8 ? "256 " : "", (long long)per_iter);
   }
   const int64_t iters = a.width / per_iter;
   const int rows_per_wave = a.block_rows / a.num_warps;
@@ -208,8 +234,8 @@ int launch_typed(const NormArgs& a) {
     SAH_NORM_CASE(16)
     default:
       return fail(SAH_ERR_UNSUPPORTED,
-                  "norm width %lld not implemented (supported: %lld x {1,2,4,8,16})",
-                  (long long)a.width, (long long)per_iter);
+                  "norm width %lld not implemented (supported: 128, %s%lld x {1,2,4,8,16})",
+                  (long long)a.width, VEC == 8 ? "256, " : "", (long long)per_iter);
   }
 #undef SAH_NORM_CASE
   return check_hip(hipGetLastError(), "norm kernel launch");

@@ -89,12 +89,16 @@ def _validate_launch_config(block_rows: int, num_warps: int) -> None:
 
 
 def supported_width(width: int, value_dtype: torch.dtype) -> bool:
-    """Widths with a kernel instantiation: 64 lanes x 16 bytes x {1, 2, 4, 8, 16}."""
+    """Widths with a kernel instantiation: 64 lanes x 16 bytes x {1, 2, 4, 8,
+    16}, and the rows narrower than one such pass (width 128; width 256 for
+    16-bit values), read with 4- or 8-byte accesses."""
 
     element_size = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}.get(value_dtype)
     if element_size is None:
         return False
     per_iteration = 64 * (16 // element_size)
+    if width in (128, 256) and width < per_iteration:
+        return True
     if width <= 0 or width % per_iteration:
         return False
     return width // per_iteration in {1, 2, 4, 8, 16}

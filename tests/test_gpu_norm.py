@@ -54,7 +54,7 @@ def _assert_gate(reference, candidate, dtype, what):
         (torch.float32, torch.bfloat16, torch.float32),
     ],
 )
-@pytest.mark.parametrize("width", [512, 1024, 2048, 4096])
+@pytest.mark.parametrize("width", [128, 256, 512, 1024, 2048, 4096])
 @pytest.mark.parametrize("rows", [1, 7, 1000])
 def test_residual_layer_norm_matches_oracle(
     gpu_device, value_dtype, update_dtype, normalized_dtype, width, rows
@@ -132,13 +132,14 @@ def test_constant_rows_return_bias(gpu_device):
     assert torch.equal(normalized.cpu(), layer_norm.bias.detach().cpu().expand(5, 512))
 
 
+@pytest.mark.parametrize("width", [128, 256, 1024])
 @pytest.mark.parametrize("block_rows,num_warps", [(1, 1), (2, 2), (4, 4), (8, 4), (16, 8), (64, 8)])
-def test_launch_shapes_are_bitwise_identical(gpu_device, block_rows, num_warps):
+def test_launch_shapes_are_bitwise_identical(gpu_device, block_rows, num_warps, width):
     module = _norm_module()
     generator = torch.Generator().manual_seed(99)
-    value = torch.randn(333, 1024, generator=generator).to(torch.bfloat16).to(gpu_device)
-    update = torch.randn(333, 1024, generator=generator).to(torch.bfloat16).to(gpu_device)
-    layer_norm = _layer_norm(1024, torch.bfloat16, 1, gpu_device)
+    value = torch.randn(333, width, generator=generator).to(torch.bfloat16).to(gpu_device)
+    update = torch.randn(333, width, generator=generator).to(torch.bfloat16).to(gpu_device)
+    layer_norm = _layer_norm(width, torch.bfloat16, 1, gpu_device)
     with torch.inference_mode():
         base = module.hip_residual_layer_norm(value, update, layer_norm, block_rows=1, num_warps=1)
         other = module.hip_residual_layer_norm(
@@ -180,11 +181,12 @@ def test_rms_norm_matches_oracle(gpu_device, dtype):
         (torch.float32, torch.bfloat16),
     ],
 )
-def test_initial_layer_norm_matches_oracle(gpu_device, value_dtype, normalized_dtype):
+@pytest.mark.parametrize("width", [128, 256, 1024])
+def test_initial_layer_norm_matches_oracle(gpu_device, value_dtype, normalized_dtype, width):
     module = _norm_module()
     generator = torch.Generator().manual_seed(8)
-    value = torch.randn(2, 513, 1024, generator=generator).to(value_dtype)
-    layer_norm = _layer_norm(1024, value_dtype, 2, gpu_device)
+    value = torch.randn(2, 513, width, generator=generator).to(value_dtype)
+    layer_norm = _layer_norm(width, value_dtype, 2, gpu_device)
     with torch.inference_mode():
         normalized, marker = module.hip_layer_norm(
             value.to(gpu_device), layer_norm, normalized_dtype=normalized_dtype
