@@ -359,6 +359,45 @@ int sah_linear_residual_norm(
  * solution/kernels/boundary/triton_linear_residual_norm.py:114-119). */
 int sah_linear_residual_norm_launch_supported(int64_t width, int block_rows, int num_warps);
 
+/*
+ * The whole FFN fused through its residual add and LayerNorm / RMSNorm
+ * boundary:
+ *   hidden     = round_to(dtype, GELU(x w1^T + b1))   (fp32 accumulation, exact GELU)
+ *   update     = round_to(dtype, hidden w2^T + b2)
+ *   residual   = round_to(dtype, value + update)
+ *   normalized = round_to(dtype, norm(residual) * gamma + beta)
+ * Neither the hidden activation nor the update reaches HBM.  For a given
+ * update, residual and normalized equal those of sah_residual_norm (same
+ * norm, parameters, eps and dtype).
+ *
+ * Replaces the reference's
+ *   _ffn_residual_norm_kernel + triton_ffn_residual_norm
+ *     (solution/kernels/boundary/triton_ffn_residual_norm.py:44-135, 211-268),
+ *   planned as FFNBackend TRITON_FUSED_MLP_BOUNDARY
+ *   (solution/plan_builder.py:783-800; solution/transformer.py:844-896).
+ * x: [rows, width] with row stride x_row_stride; w1: [ffn, width] and w2:
+ * [width, ffn] contiguous (the ffn_in / ffn_out weights); b1 [ffn], b2, gamma,
+ * beta [width], each may be NULL (0, 0, 1, 0); value, residual, normalized:
+ * [rows, width] contiguous, residual and normalized not aliasing any input.
+ * Shared dtype SAH_DTYPE_BF16 or SAH_DTYPE_F16; norm_kind SAH_NORM_LAYER or
+ * SAH_NORM_RMS.  width 128 or 256 (the reference's kernel: 128), ffn a
+ * multiple of 64; x_row_stride a multiple of 8; tensors 16-byte aligned,
+ * biases 8-byte.  Launch: block_rows = 64 rows per workgroup of num_warps = 4
+ * wavefronts, see sah_mlp_residual_norm_launch_supported().
+ */
+int sah_mlp_residual_norm(
+    const void* x, const void* w1, const void* b1, const void* w2, const void* b2,
+    const void* value, const void* gamma, const void* beta,
+    void* residual, void* normalized,
+    int64_t rows, int64_t width, int64_t ffn, int64_t x_row_stride,
+    float eps, int dtype, int norm_kind, int block_rows, int num_warps,
+    sah_stream_t stream);
+
+/* 1 if sah_mlp_residual_norm implements (width, block_rows, num_warps), else 0
+ * (mirrors the reference's _launch_is_valid,
+ * solution/kernels/boundary/triton_ffn_residual_norm.py:30-38). */
+int sah_mlp_residual_norm_launch_supported(int64_t width, int block_rows, int num_warps);
+
 #ifdef __cplusplus
 }
 #endif

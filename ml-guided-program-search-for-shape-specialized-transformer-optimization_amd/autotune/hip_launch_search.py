@@ -15,8 +15,9 @@ build:
   never timed);
 * it is a coordinate search: attention launch, then norm launch, then the FFN
   activation path (hipBLASLt + torch GELU, hipBLASLt + the HIP elementwise
-  GELU, or the fused HIP Linear + exact-GELU kernel where the plan builder
-  accepts it), then the QKV path (hipBLASLt packed projection with zero-copy
+  GELU, the fused HIP Linear + exact-GELU kernel, or the whole FFN fused
+  through its residual LayerNorm, where the plan builder accepts them), then
+  the QKV path (hipBLASLt packed projection with zero-copy
   views, the HIP projection writing head-major Q / K and the attention's
   V^T layout, or that projection with the initial LayerNorm fused in), then
   the residual boundary (hipBLASLt output projections
@@ -63,6 +64,7 @@ from autotune.accuracy import no_less_accurate
 from solution.config import (
     HIP_GELU_LAUNCH,
     HIP_LINEAR_LAUNCH,
+    HIP_MLP_BOUNDARY_LAUNCH,
     HIP_QKV_LAUNCH,
     AttentionLaunchParams,
     ConfigSpec,
@@ -142,22 +144,24 @@ def _with_attention(config: ConfigSpec, launch: AttentionLaunchParams) -> Config
 
 def _ffn_variants(config: ConfigSpec) -> list[ConfigSpec]:
     """The FFN activation paths: hipBLASLt followed by torch's GELU or by the
-    HIP elementwise GELU, or the fused HIP Linear + bias + exact-GELU kernel,
-    each with its launch."""
+    HIP elementwise GELU, the fused HIP Linear + bias + exact-GELU kernel,
+    each with its launch, and the whole FFN fused through its residual
+    LayerNorm (whose launch is also the residual norms'; legal only at the
+    widths that kernel serves)."""
 
-    def with_ffn(backend: FFNBackend, ffn_launch=None, ffn_input_launch=None) -> ConfigSpec:
+    def with_ffn(backend: FFNBackend, ffn_launch=None, ffn_input_launch=None, residual_norm_launch=None) -> ConfigSpec:
+        schedule = dataclasses.replace(config.schedule, ffn_launch=ffn_launch, ffn_input_launch=ffn_input_launch)
+        if residual_norm_launch is not None:
+            schedule = dataclasses.replace(schedule, residual_norm_launch=residual_norm_launch)
         return dataclasses.replace(
-            config,
-            program=dataclasses.replace(config.program, ffn=backend),
-            schedule=dataclasses.replace(
-                config.schedule, ffn_launch=ffn_launch, ffn_input_launch=ffn_input_launch
-            ),
+            config, program=dataclasses.replace(config.program, ffn=backend), schedule=schedule
         )
 
     return [
         with_ffn(FFNBackend.TORCH),
         with_ffn(FFNBackend.HIP_EXACT_GELU, ffn_launch=HIP_GELU_LAUNCH),
         with_ffn(FFNBackend.HIP_LINEAR_EXACT_GELU, ffn_input_launch=HIP_LINEAR_LAUNCH),
+        with_ffn(FFNBackend.HIP_FUSED_MLP_BOUNDARY, residual_norm_launch=HIP_MLP_BOUNDARY_LAUNCH),
     ]
 
 

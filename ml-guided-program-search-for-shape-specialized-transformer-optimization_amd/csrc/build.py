@@ -31,6 +31,7 @@ SOURCES = (
     "linear_gelu.hip",
     "gelu.hip",
     "linear_norm.hip",
+    "mlp_norm.hip",
 )
 OFFLOAD_ARCH = "gfx950"
 

@@ -20,6 +20,9 @@ the schema (version 4) is unchanged:
   rows per workgroup of num_warps wavefronts).
 * ``InitialNormBackend.HIP`` - the layer-0 LayerNorm; launch in
   ``initial_norm_launch``.
+* ``FFNBackend.HIP_FUSED_MLP_BOUNDARY`` - the whole FFN fused through its
+  residual add and LayerNorm (the reference's ``TRITON_FUSED_MLP_BOUNDARY``);
+  like it, the kernel's launch is ``residual_norm_launch``.
 * ``InitialNormBackend.HIP_FUSED_QKV`` - the layer-0 LayerNorm fused into the
   HIP native-layout QKV projection (the reference's ``TRITON_FUSED_QKV``);
   like it, no ``initial_norm_launch``: it runs with ``qkv_launch``.
@@ -99,6 +102,7 @@ class FFNBackend(_StrEnum):
     TRITON_FUSED_MLP_BOUNDARY = "triton_fused_mlp_boundary"
     HIP_LINEAR_EXACT_GELU = "hip_linear_exact_gelu"
     HIP_EXACT_GELU = "hip_exact_gelu"
+    HIP_FUSED_MLP_BOUNDARY = "hip_fused_mlp_boundary"
 
 
 class ResidualNormBackend(_StrEnum):
@@ -676,6 +680,9 @@ HIP_LINEAR_LAUNCH = GemmLaunchParams(block_m=256, block_n=256, block_k=64, num_w
 # 16-byte chunk per thread, 8 wavefronts (6.1 TB/s on the C5 hidden tensor,
 # the fastest of the implemented launches on MI355X).
 HIP_GELU_LAUNCH = FFNLaunchParams(block_size=4096, num_warps=8)
+# The fused MLP boundary's launch (64 rows per workgroup of 4 wavefronts),
+# also a valid launch of the fused residual norm at the attention boundary.
+HIP_MLP_BOUNDARY_LAUNCH = NormLaunchParams(block_rows=64, num_warps=4)
 # The launch of the HIP packed-QKV projection with the head-major epilogue
 # (csrc/linear_gelu.hip, sah_qkv_projection): the same GEMM core.
 HIP_QKV_LAUNCH = QKVLaunchParams(block_m=256, block_n=256, block_k=64, num_warps=8)
@@ -706,8 +713,11 @@ def hip_config(
     the FFN activation by the HIP exact-GELU kernel.  ``microbatch_size`` selects the streamed schedule, ``graph``
     the graph-replay runtime (one HIP graph per input signature).  ``ffn``
     picks the FFN activation path: TORCH (hipBLASLt, then torch's exact GELU),
-    HIP_EXACT_GELU (hipBLASLt, then the HIP elementwise GELU) or
-    HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU).  ``qkv``
+    HIP_EXACT_GELU (hipBLASLt, then the HIP elementwise GELU),
+    HIP_LINEAR_EXACT_GELU (the fused HIP Linear + bias + exact GELU) or
+    HIP_FUSED_MLP_BOUNDARY (the whole FFN and its residual LayerNorm in one
+    kernel, widths 128 and 256; its launch HIP_MLP_BOUNDARY_LAUNCH is also the
+    attention boundary's norm launch).  ``qkv``
     picks how Q, K and V are produced: VIEW (hipBLASLt packed projection and
     zero-copy views) or HIP_NATIVE_BHSD (the HIP projection writing
     head-major Q / K and a seq-contiguous V straight from its epilogue).
@@ -719,7 +729,12 @@ def hip_config(
     (fused into the HIP_NATIVE_BHSD projection, which it requires)."""
 
     ffn = FFNBackend(ffn)
-    if ffn not in {FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU}:
+    if ffn not in {
+        FFNBackend.TORCH,
+        FFNBackend.HIP_EXACT_GELU,
+        FFNBackend.HIP_LINEAR_EXACT_GELU,
+        FFNBackend.HIP_FUSED_MLP_BOUNDARY,
+    }:
         raise ValueError(f"FFN backend {ffn.value!r} is not part of the gfx950 program")
     qkv = QKVMaterialization(qkv)
     if qkv not in {QKVMaterialization.VIEW, QKVMaterialization.HIP_NATIVE_BHSD}:
@@ -737,9 +752,12 @@ def hip_config(
     elif residual_norm is ResidualNormBackend.HIP_FUSED:
         if boundary_launch is not None:
             raise ValueError("boundary_launch is only for the linear boundary")
-        residual_launch = norm_launch
+        # the fused MLP boundary runs with the residual-norm launch
+        residual_launch = HIP_MLP_BOUNDARY_LAUNCH if ffn is FFNBackend.HIP_FUSED_MLP_BOUNDARY else norm_launch
     else:
         raise ValueError(f"residual norm {residual_norm.value!r} is not part of the gfx950 program")
+    if ffn is FFNBackend.HIP_FUSED_MLP_BOUNDARY and residual_norm is not ResidualNormBackend.HIP_FUSED:
+        raise ValueError("the fused MLP boundary pairs with the HIP_FUSED attention boundary")
 
     if graph and microbatch_size is not None:
         raise ValueError("the graph runtime and the streamed schedule are exclusive")
@@ -783,6 +801,7 @@ __all__ = [
     "HIP_DEFAULT_ATTENTION_LAUNCH",
     "HIP_DEFAULT_NORM_LAUNCH",
     "HIP_GELU_LAUNCH",
+    "HIP_MLP_BOUNDARY_LAUNCH",
     "HIP_LINEAR_LAUNCH",
     "HIP_QKV_LAUNCH",
     "HIP_LONG_SEQUENCE_ATTENTION_LAUNCH",

@@ -99,6 +99,11 @@ _SIGNATURES: dict[str, tuple[list[object], object]] = {
         _int,
     ),
     "sah_linear_residual_norm_launch_supported": ([_i64, _int, _int], _int),
+    "sah_mlp_residual_norm": (
+        [_ptr] * 10 + [_i64] * 4 + [ctypes.c_float] + [_int] * 4 + [_ptr],
+        _int,
+    ),
+    "sah_mlp_residual_norm_launch_supported": ([_i64, _int, _int], _int),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 # SAH_ATTENTION_STATIC_WORKSPACE_BYTES of the header: the device array behind

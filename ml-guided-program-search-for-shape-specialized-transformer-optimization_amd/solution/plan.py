@@ -221,6 +221,13 @@ class ExecutionPlan:
         return self.initial_norm_backend is InitialNormBackend.HIP_FUSED_QKV
 
     @property
+    def use_fused_mlp_boundary(self) -> bool:
+        """The FFN and its residual LayerNorm run as one kernel (reference
+        :843-896)."""
+
+        return self.ffn_backend is FFNBackend.HIP_FUSED_MLP_BOUNDARY
+
+    @property
     def use_hip_residual_norm(self) -> bool:
         return self.residual_norm_backend in {
             ResidualNormBackend.HIP_FUSED,

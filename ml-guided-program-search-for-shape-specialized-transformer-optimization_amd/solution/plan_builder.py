@@ -143,6 +143,7 @@ class HardwareCapabilities:
     hip_exact_gelu: bool = False
     hip_qkv_native_bhsd: bool = False
     hip_linear_residual_norm: bool = False
+    hip_mlp_residual_norm: bool = False
 
     @property
     def is_gfx950(self) -> bool:
@@ -193,6 +194,7 @@ class HardwareCapabilities:
             hip_exact_gelu=hip_available,
             hip_qkv_native_bhsd=hip_available,
             hip_linear_residual_norm=hip_available,
+            hip_mlp_residual_norm=hip_available,
         )
 
 
@@ -548,8 +550,66 @@ class PlanBuilder:
                     "HIP Linear + Exact-GELU implements (256, 256, 64, 8, 2)",
                 )
             return
+        if backend is FFNBackend.HIP_FUSED_MLP_BOUNDARY:
+            PlanBuilder._validate_fused_mlp_boundary(config, context, hardware, reject)
+            return
         what = "torch.compile FFN" if backend is FFNBackend.COMPILED else f"Triton FFN {backend.value}"
         _unavailable(reject, "program.ffn", what)
+
+    @staticmethod
+    def _validate_fused_mlp_boundary(
+        config: ConfigSpec,
+        context: ExecutionContext,
+        hardware: HardwareCapabilities,
+        reject: Reject,
+    ) -> None:
+        """The reference's TRITON_FUSED_MLP_BOUNDARY rules (solution/
+        plan_builder.py:783-800): the kernel's widths, native-dtype FFN
+        weights, the launch carried by residual_norm_launch.  The reference
+        pairs it with its fused linear boundary at the attention output; here
+        the pair is the fused residual norm (HIP_FUSED), because the HIP
+        linear boundary has no kernel at these widths."""
+
+        from .kernels.boundary.hip_mlp_residual_norm import launch_config_is_valid, supported_shape
+
+        field = "program.ffn"
+        _validate_hip_common(context, hardware, hardware.hip_mlp_residual_norm, field, reject)
+        if context.dtype not in {torch.float16, torch.bfloat16}:
+            reject("unsupported_dtype", field, "the fused MLP boundary runs on FP16 and BF16 models")
+        if context.ffn_dim is None or not supported_shape(context.d_model, context.ffn_dim):
+            reject(
+                "unsupported_shape",
+                field,
+                "the fused MLP boundary supports d_model 128 and 256 with ffn_dim % 64 == 0",
+            )
+        for name in ("ffn_input_projection", "ffn_output_projection"):
+            if getattr(config.program, name) is not ProjectionBackend.INPUT_DTYPE:
+                reject(
+                    "backend_incompatible",
+                    f"program.{name}",
+                    "the fused MLP boundary multiplies the native-dtype FFN weights",
+                )
+        if config.program.precision_plan is not PrecisionPlan.INPUT_DTYPE:
+            reject(
+                "backend_incompatible",
+                "program.precision_plan",
+                "the fused MLP boundary keeps the hidden activation in the model dtype",
+            )
+        if config.program.residual_norm is not ResidualNormBackend.HIP_FUSED:
+            reject(
+                "backend_incompatible",
+                "program.residual_norm",
+                "the fused MLP boundary pairs with the HIP fused residual norm",
+            )
+        if config.schedule.runtime is RuntimeBackend.COMPILED_FORWARD:
+            reject("runtime_incompatible", "schedule.runtime", "the fused MLP boundary is not nested in compiled forward")
+        launch = config.schedule.residual_norm_launch
+        if launch is None or not launch_config_is_valid(context.d_model, launch.block_rows, launch.num_warps):
+            reject(
+                "unsupported_launch_value",
+                "schedule.residual_norm_launch",
+                "the fused MLP boundary runs 64 rows per workgroup of 4 wavefronts",
+            )
 
     # ------------------------------------------------------------ residual norm
     @staticmethod

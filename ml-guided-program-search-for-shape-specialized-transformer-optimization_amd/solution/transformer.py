@@ -563,6 +563,65 @@ class _TransformerBlock(nn.Module):
         return update
 
 
+    def mlp_boundary(
+        self,
+        normalized: torch.Tensor,
+        value: torch.Tensor,
+        next_norm: nn.LayerNorm,
+        plan: ExecutionPlan,
+        observation: _ExecutionObservation | None,
+        *,
+        out: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """The whole FFN and the residual LayerNorm after it in one kernel
+        (reference: the TRITON_FUSED_MLP_BOUNDARY branch,
+        solution/transformer.py:843-896, here the gfx950 kernel); neither the
+        hidden activation nor the update reaches HBM."""
+
+        from .kernels.boundary.hip_mlp_residual_norm import (
+            HIP_MLP_RESIDUAL_NORM_BACKEND,
+            hip_mlp_residual_norm,
+        )
+
+        launch = plan.residual_norm_launch
+        if launch is None:
+            raise RuntimeError("fused MLP boundary is missing launch parameters")
+        destination = (
+            out if out is not None and out.dtype == value.dtype and out.is_contiguous() else None
+        )
+        value, normalized, marker = hip_mlp_residual_norm(
+            normalized,
+            self.ffn_in.weight,
+            self.ffn_in.bias,
+            self.ffn_out.weight,
+            self.ffn_out.bias,
+            value,
+            next_norm,
+            block_rows=launch.block_rows,
+            num_warps=launch.num_warps,
+            out=destination,
+        )
+        _strict_backend_marker(
+            marker,
+            expected_marker=HIP_MLP_RESIDUAL_NORM_BACKEND,
+            planned_backend=plan.ffn_backend.value,
+        )
+        if observation is not None:
+            dtype = _dtype_name(value.dtype)
+            observation.ffn_input_projection_backends.append(plan.ffn_input_projection_backend.value)
+            observation.ffn_input_projection_compute_dtypes.append(dtype)
+            observation.ffn_activation_output_dtypes.append(dtype)
+            observation.ffn_output_projection_backends.append(plan.ffn_output_projection_backend.value)
+            observation.ffn_output_projection_compute_dtypes.append(dtype)
+            observation.ffn_launches.append(None)
+            observation.ffn_input_launches.append(None)
+            observation.ffn_backends.append(plan.ffn_backend.value)
+            # the FFN boundary's residual norm runs inside the fused kernel
+            observation.residual_norm_backends.append(plan.residual_norm_backend.value)
+            observation.residual_norm_launches.append(_launch_dict(plan.residual_norm_launch))
+        return value, normalized
+
+
 class UserOptimizedTransformer(nn.Module):
     """Solution entry with the official constructor and forward API."""
 
@@ -907,17 +966,22 @@ class UserOptimizedTransformer(nn.Module):
                 value, normalized = self._apply_residual_norm(
                     value, update, layer.norm2, valid_token_mask, plan, observation, final_boundary=False
                 )
-                update = layer.ffn_update(normalized, plan, observation)
-                value, normalized = self._apply_residual_norm(
-                    value,
-                    update,
-                    next_norm,
-                    valid_token_mask,
-                    plan,
-                    observation,
-                    final_boundary=last,
-                    out=out if last else None,
-                )
+                if plan.use_fused_mlp_boundary:
+                    value, normalized = layer.mlp_boundary(
+                        normalized, value, next_norm, plan, observation, out=out if last else None
+                    )
+                else:
+                    update = layer.ffn_update(normalized, plan, observation)
+                    value, normalized = self._apply_residual_norm(
+                        value,
+                        update,
+                        next_norm,
+                        valid_token_mask,
+                        plan,
+                        observation,
+                        final_boundary=last,
+                        out=out if last else None,
+                    )
             if observation is not None:
                 observation.layer_output_dtypes.append(_dtype_name(normalized.dtype))
         if valid_token_mask is not None:

@@ -35,7 +35,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         triton_mixed_residual_norm=False, triton_initial_norm=False, triton_exact_gelu=False,
         triton_streaming_dh64_attention=False, gcn_arch="gfx950", hip_streaming_dh64_attention=True,
         hip_residual_norm=True, hip_initial_norm=True, hip_exact_gelu=True, hip_linear_exact_gelu=True,
-        hip_qkv_native_bhsd=True, hip_linear_residual_norm=True,
+        hip_qkv_native_bhsd=True, hip_linear_residual_norm=True, hip_mlp_residual_norm=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -136,10 +136,17 @@ def test_ffn_stage_offers_hipblaslt_and_the_fused_kernel():
     variants = _ffn_variants(base)
     assert [v.program.ffn for v in variants] == [
         FFNBackend.TORCH, FFNBackend.HIP_EXACT_GELU, FFNBackend.HIP_LINEAR_EXACT_GELU,
+        FFNBackend.HIP_FUSED_MLP_BOUNDARY,
     ]
     assert variants[1] == base  # the default program is one of them
     device = torch.device("cuda")
-    assert all(search.legal(v, device) for v in variants)
+    assert all(search.legal(v, device) for v in variants[:3])
+    # the fused MLP boundary serves widths 128 and 256 only: offered, never timed here
+    assert not search.legal(variants[3], device)
+    small = HipLaunchSearch(torch.nn.Identity(), SearchShape(8, 128, 256, 4, 1024, 2), hardware=_gfx950())
+    small_variants = _ffn_variants(small.incumbent())
+    assert small.legal(small_variants[3], device)
+    assert small_variants[3].schedule.residual_norm_launch.to_dict() == {"block_rows": 64, "num_warps": 4}
     # without the kernels the HIP variants are rejected, never timed
     no_kernel = HipLaunchSearch(
         torch.nn.Identity(), shape, hardware=_gfx950(hip_exact_gelu=False, hip_linear_exact_gelu=False)

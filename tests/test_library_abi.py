@@ -238,3 +238,43 @@ def test_norm_qkv_projection_entry_validates_before_launch():
     assert call(ws_bytes=1599) == _library.SAH_ERR_WORKSPACE and b"1600" in library.sah_last_error()
     assert call(ws=None) == _library.SAH_ERR_WORKSPACE
     assert call(ws=ctypes.c_void_p(4096 + 8)) == _library.SAH_ERR_WORKSPACE
+
+
+def test_mlp_residual_norm_entry_validates_before_launch():
+    """sah_mlp_residual_norm's launch table and argument checks (no kernel runs)."""
+
+    from solution.kernels.boundary.hip_mlp_residual_norm import launch_config_is_valid, supported_shape
+
+    library = _library.load_library()
+    for width in (128, 256):
+        assert library.sah_mlp_residual_norm_launch_supported(width, 64, 4) == 1
+        assert launch_config_is_valid(width, 64, 4)
+    for launch in [(512, 64, 4), (256, 32, 4), (256, 64, 8), (1024, 64, 4)]:
+        assert library.sah_mlp_residual_norm_launch_supported(*launch) == 0
+        assert not launch_config_is_valid(*launch)
+    assert supported_shape(128, 128) and supported_shape(256, 1024) and not supported_shape(256, 1000)
+    assert not supported_shape(512, 2048)
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    base = dict(rows=100, width=256, ffn=1024, ldx=256, eps=1e-5, dtype=2, kind=_library.SAH_NORM_LAYER,
+                launch=(64, 4), x=fake, b1=None)
+
+    def call(**over):
+        a = {**base, **over}
+        return library.sah_mlp_residual_norm(a["x"], fake, a["b1"], fake, None, fake, None, None, fake, fake,
+                                             a["rows"], a["width"], a["ffn"], a["ldx"], a["eps"], a["dtype"],
+                                             a["kind"], *a["launch"], None)
+
+    assert call(width=512, ldx=512) == _library.SAH_ERR_UNSUPPORTED
+    assert library.sah_last_error().startswith(b"sah_mlp_residual_norm:")
+    assert call(launch=(32, 4)) == _library.SAH_ERR_UNSUPPORTED
+    assert call(dtype=0) == _library.SAH_ERR_UNSUPPORTED
+    assert call(kind=7) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ffn=1000) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ffn=0) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(rows=-1) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(ldx=200) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(eps=float("inf")) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(rows=0) == _library.SAH_OK  # nothing to do, nothing launched
+    assert call(x=None) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(x=ctypes.c_void_p(4096 + 8)) == _library.SAH_ERR_INVALID_ARGUMENT
+    assert call(b1=ctypes.c_void_p(4096 + 4)) == _library.SAH_ERR_INVALID_ARGUMENT

@@ -59,6 +59,7 @@ def _gfx950(**overrides) -> HardwareCapabilities:
         hip_exact_gelu=True,
         hip_qkv_native_bhsd=True,
         hip_linear_residual_norm=True,
+        hip_mlp_residual_norm=True,
     )
     values.update(overrides)
     return HardwareCapabilities(**values)
@@ -532,6 +533,85 @@ def test_fused_initial_norm_qkv_plans_and_rejections():
         fused, program=dataclasses.replace(fused.program, initial_norm=InitialNormBackend.TRITON_FUSED_QKV)
     )
     assert ("program.initial_norm", "backend_unavailable") in codes(builder.evaluate(triton, c2, _gfx950()))
+
+
+def test_fused_mlp_boundary_plans_and_rejections():
+    """The whole FFN fused through its residual LayerNorm (the reference's
+    TRITON_FUSED_MLP_BOUNDARY rules, solution/plan_builder.py:783-800): the
+    kernel's widths, native-dtype FFN weights, the launch carried by
+    residual_norm_launch, paired with the HIP fused residual norm."""
+
+    from solution.config import HIP_MLP_BOUNDARY_LAUNCH, FFNBackend, PrecisionPlan, ProjectionBackend
+
+    builder = PlanBuilder()
+    codes = lambda result: {(v.field, v.code) for v in result.violations}  # noqa: E731
+    fused = hip_config(ffn=FFNBackend.HIP_FUSED_MLP_BOUNDARY)
+    assert fused.program.ffn is FFNBackend.HIP_FUSED_MLP_BOUNDARY
+    assert fused.schedule.residual_norm_launch == HIP_MLP_BOUNDARY_LAUNCH == NormLaunchParams(64, 4)
+    assert fused.schedule.ffn_launch is None and fused.schedule.ffn_input_launch is None
+    assert ConfigSpec.from_dict(fused.to_dict()) == fused
+    assert fused.to_dict()["program"]["ffn"] == "hip_fused_mlp_boundary"
+    small = _context(batch=8, seq=128, d=256, heads=4, ffn=1024, layers=2)
+    plan = builder.build(fused, small, _gfx950())
+    assert plan.use_fused_mlp_boundary
+    trace = plan.expected_trace.to_dict()
+    assert trace["ffn_backend"] == "hip_fused_mlp_boundary" and trace["residual_norm_calls"] == 4
+    # the reference's own width
+    assert builder.build(fused, _context(batch=64, seq=128, d=128, heads=2, ffn=128, layers=2), _gfx950())
+    with pytest.raises(ValueError, match="HIP_FUSED attention boundary"):
+        from solution.config import ResidualNormBackend, hip_linear_boundary_launch
+
+        hip_config(
+            ffn=FFNBackend.HIP_FUSED_MLP_BOUNDARY,
+            residual_norm=ResidualNormBackend.HIP_LINEAR_FUSED,
+            boundary_launch=hip_linear_boundary_launch(512),
+        )
+    wide = builder.evaluate(fused, _context(batch=2, seq=256, d=512, heads=8, ffn=2048), _gfx950())
+    assert ("program.ffn", "unsupported_shape") in codes(wide)
+    odd_ffn = builder.evaluate(fused, _context(batch=8, seq=128, d=256, heads=4, ffn=1000), _gfx950())
+    assert ("program.ffn", "unsupported_shape") in codes(odd_ffn)
+    fp32 = builder.evaluate(fused, _context(batch=8, seq=128, d=256, heads=4, ffn=1024, dtype=torch.float32), _gfx950())
+    assert ("program.ffn", "unsupported_dtype") in codes(fp32)
+    masked = builder.evaluate(fused, _context(batch=8, seq=128, d=256, heads=4, ffn=1024, mask=True), _gfx950())
+    assert ("program.ffn", "mask_not_supported") in codes(masked)
+    unavailable = builder.evaluate(fused, small, _gfx950(hip_mlp_residual_norm=False))
+    assert ("program.ffn", "backend_unavailable") in codes(unavailable)
+    wrong_launch = dataclasses.replace(
+        fused, schedule=dataclasses.replace(fused.schedule, residual_norm_launch=NormLaunchParams(4, 4))
+    )
+    assert ("schedule.residual_norm_launch", "unsupported_launch_value") in codes(
+        builder.evaluate(wrong_launch, small, _gfx950())
+    )
+    shadow = dataclasses.replace(
+        fused,
+        program=dataclasses.replace(
+            fused.program,
+            precision_plan=PrecisionPlan.FP16_FFN_INPUT_FP32_GELU,
+            ffn_input_projection=ProjectionBackend.FP16_SHADOW,
+        ),
+    )
+    assert ("program.ffn_input_projection", "backend_incompatible") in codes(builder.evaluate(shadow, small, _gfx950()))
+    torch_norm = dataclasses.replace(
+        fused,
+        program=dataclasses.replace(fused.program, residual_norm=ResidualNormBackend.TORCH),
+        schedule=dataclasses.replace(fused.schedule, residual_norm_launch=None),
+    )
+    assert ("program.residual_norm", "backend_incompatible") in codes(builder.evaluate(torch_norm, small, _gfx950()))
+    # the reference's Triton fusion stays unavailable, not replaced
+    triton = dataclasses.replace(
+        fused, program=dataclasses.replace(fused.program, ffn=FFNBackend.TRITON_FUSED_MLP_BOUNDARY)
+    )
+    assert ("program.ffn", "backend_unavailable") in codes(builder.evaluate(triton, small, _gfx950()))
+
+
+def test_narrow_widths_have_hip_norms():
+    """The fused norm kernel covers 16-bit widths 128 and 256, so the gfx950
+    program is legal at them."""
+
+    builder = PlanBuilder()
+    for width, heads in ((128, 2), (256, 4)):
+        plan = builder.build(hip_config(), _context(batch=8, seq=128, d=width, heads=heads, ffn=4 * width), _gfx950())
+        assert plan.use_hip_residual_norm
 
 
 def test_linear_boundary_plans_and_rejections():
