@@ -71,10 +71,14 @@ const char* sah_last_error(void);
  *      kernel then first writes V^T into `workspace`) or seq-contiguous
  *      (v_stride_s == 1, a V^T buffer).
  * workspace: 16-byte aligned, at least sah_causal_attention_workspace_bytes();
- *      may be null when that is 0.  Sequences of 16384 keys or more keep a
- *      table of the largest key norm of every 64-key tile there (written by a
- *      pre-pass over K), which bounds every score so that most tiles skip
- *      their row maximum.
+ *      may be null when that is 0.  Sequences of 16384 keys or more keep
+ *      there, written by a pre-pass over K and Q: tables of the largest key
+ *      norm and query norm of every 64-row tile, which bound every score so
+ *      that most tiles skip their row maximum, and the keys times
+ *      scale * log2(e) in fp16.  A block of 512 query rows whose bound
+ *      scale * log2(e) * max|q| * max|k| is at most 32 (15 for fp16) computes
+ *      its scores on the fp16 MFMA from those keys and takes P = exp2(score)
+ *      without a shift; other blocks keep the shifted path.
  * out: [B, S, H*64], element stride 1 on the feature axis.
  * Launch parameters: (block_m query rows, num_warps wavefronts) per workgroup
  *      in {(128, 4), (256, 4), (256, 8), (512, 8)} (32 or 64 query rows per
@@ -94,10 +98,11 @@ int sah_causal_attention_bsd(
     void* workspace, size_t workspace_bytes,
     sah_stream_t stream);
 
-/* Workspace bytes sah_causal_attention_bsd needs: the key-norm table for
- * seq_len >= 16384 (4 bytes per 64-key tile per head, rounded up to 256),
- * then V^T when value is head_dim-contiguous; 0 for a seq-contiguous value
- * shorter than 16384 keys. */
+/* Workspace bytes sah_causal_attention_bsd needs: for seq_len >= 16384 the
+ * key-norm and query-norm tables (4 bytes per 64-row tile per head, each
+ * rounded up to 256) and the fp16 scaled keys (128 bytes per key, seq_len
+ * rounded up to 64, per head), then V^T when value is head_dim-contiguous;
+ * 0 for a seq-contiguous value shorter than 16384 keys. */
 size_t sah_causal_attention_workspace_bytes(
     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
     int64_t v_stride_s, int64_t v_stride_d, int dtype);

@@ -70,6 +70,32 @@ template <typename T>
 constexpr float safe_exponent() {
   return std::is_same<T, f16>::value ? 15.0f : 64.0f;
 }
+// Scaled-key path (plain kernel, with the key-norm pre-pass).  The pre-pass
+// also writes every key multiplied by c and rounded to fp16 (11-bit mantissa),
+// and a block of query rows whose largest c |q| max|k| is at most this bound
+// (over the keys it reads) runs its tiles on the fp16 MFMA with Q in fp16:
+// the MFMA then yields the log2-domain score c q.k itself, and since every
+// such score lies in [-bound, bound], P = exp2(score) needs neither a shift
+// nor a row maximum (bf16 P: 2^32 is far inside the fp32 exponent range; fp16
+// P: 2^15 < 65504).  Softmax is shift-invariant; only the point where P is
+// rounded to 16 bits moves, and the relative rounding error of P is the same
+// at any exponent.  The fp16 key product adds at most 2^-12 relative per term,
+// under a quarter of a bf16 ulp of P at the bound.  Blocks with a larger
+// bound (large-magnitude inputs, an outlier key or query) keep the shifted
+// path on the original keys.
+template <typename T>
+constexpr float scaled_key_bound() {
+  return std::is_same<T, f16>::value ? 15.0f : 32.0f;
+}
+// |q| and c max|k| must also stay below this for the fp16 operands: no
+// overflow, and fp16 subnormals of the other operand contribute at most
+// 8 * 4096 * 2^-25 = 2^-10 to a score.
+constexpr float kScaledKeyMaxNorm = 4096.0f;
+// The path is chosen per block of this many query rows (a multiple of every
+// plain launch's block_m), from that block's largest |q| and the largest |k|
+// of the keys it reads, so every launch takes the same path for a row and the
+// results stay independent of the launch.
+constexpr int kScaledKeyRows = 512;
 // Sequences at least this long get the key-norm pre-pass (one extra read of
 // K).  Measured on MI355X, bf16, pre-pass included: 40.51 -> 38.93 ms on the
 // long-sequence chunk (B2 H16 S100000), 0.645 -> 0.633 ms at B1 H16 S16384,
@@ -105,6 +131,11 @@ struct AttnParams {
   // its row maximum.
   const float* knorm;
   int key_tiles;
+  // Keys times c in fp16, [batch*heads][key_tiles * 64][64] (rows past the
+  // sequence never read), written by the pre-pass; null without it.
+  const f16* kc;
+  // Largest |q| of every 64-row tile, laid out as knorm; set with kc.
+  const float* qnorm;
 };
 
 // Workgroup id -> (batch*head, query tile).  With head_group G > 0, XCD x
@@ -194,7 +225,16 @@ constexpr int attn_min_waves_per_simd() {
   return (QG == 1 && WAVES == 8 && STAGES == 2) ? 4 : 1;
 }
 
-template <typename T, int QG, int STAGES, int WAVES>
+// PATH: kPathAll runs every workgroup on the shifted path (no scaled keys);
+// with the scaled keys, kPathScaled runs the workgroups that qualify for the
+// scaled-key path and kPathShifted the others, as two launches over the same
+// grid (each kernel keeps one copy of the tile loop: both copies in one
+// kernel raised its register use past the 4-wave-per-SIMD budget).
+constexpr int kPathAll = 0;
+constexpr int kPathScaled = 1;
+constexpr int kPathShifted = 2;
+
+template <typename T, int QG, int STAGES, int WAVES, int PATH>
 __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES, WAVES>())) void attn_fwd_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
@@ -260,6 +300,11 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     qnc[g] = sqrtf(half_swap_sum(ss)) * p.c;
   }
 
+  // Key source: the keys as given, or the pre-pass's fp16 keys times c on the
+  // scaled-key path (chosen below, before the first tile is staged).
+  const T* kb = kbase;
+  int64_t kss = p.k_ss;
+
   // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
   u32x4 k_pref[CPT], v_pref[CPT];
   auto load_tile = [&](int tile) {
@@ -270,7 +315,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
         const int chunk = tid + NT * i;
         const int row = chunk >> 3;
         const int c8 = (chunk & 7) * 8;
-        k_pref[i] = load16(kbase + (int64_t)(k0 + row) * p.k_ss + c8);
+        k_pref[i] = load16(kb + (int64_t)(k0 + row) * kss + c8);
         v_pref[i] = load16(vbase + (int64_t)row * p.v_sd + k0 + c8);
       }
     } else {
@@ -281,7 +326,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
         const int c8 = (chunk & 7) * 8;
         const int key = k0 + row;
         u32x4 raw = {0u, 0u, 0u, 0u};
-        if (key < S) raw = load16(kbase + (int64_t)key * p.k_ss + c8);
+        if (key < S) raw = load16(kb + (int64_t)key * kss + c8);
         k_pref[i] = raw;
         // V^T: row = head-dim index, 8 consecutive keys.
         v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
@@ -314,10 +359,6 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   }
   const float c = p.c;
   const int a_row = k_row_for(l32);
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
   const bool bounded = p.knorm != nullptr;  // uniform
   // Global address space spelled out: the table entry of the next tile is
   // then a scalar load (uniform address, read-only).  Left to inference the
@@ -325,6 +366,51 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   // of the loop also waited for (6% slower on the long-sequence chunk).
   typedef const __attribute__((address_space(1))) float* GlobalFloats;
   GlobalFloats knorm = bounded ? (GlobalFloats)p.knorm + (int64_t)bh * p.key_tiles : nullptr;
+
+  // ---- scaled-key path: taken by the block of kScaledKeyRows query rows
+  // that holds this workgroup's rows when c max|q| max|k| <= scaled_key_bound
+  // over the block's rows and the keys they read (and both operands fit fp16
+  // comfortably).  Every wave forms the same exact maxima, so the workgroup
+  // returns as a whole or not at all.
+  constexpr bool SCALED = PATH == kPathScaled;
+  if constexpr (PATH != kPathAll) {  // the host launches these only with the tables
+    const int row0 = (q0 / kScaledKeyRows) * kScaledKeyRows;
+    const int block_tiles = (min(row0 + kScaledKeyRows, S) + kBlockN - 1) / kBlockN;
+    GlobalFloats qnorm = (GlobalFloats)p.qnorm + (int64_t)bh * p.key_tiles;
+    float kmax = 0.0f, qmax = 0.0f;
+    for (int t = lane; t < block_tiles; t += 64) kmax = fmaxf(kmax, knorm[t]);
+    for (int t = row0 / kBlockN + lane; t < block_tiles; t += 64) qmax = fmaxf(qmax, qnorm[t]);
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+      kmax = fmaxf(kmax, __shfl_xor(kmax, offset));
+      qmax = fmaxf(qmax, __shfl_xor(qmax, offset));
+    }
+    const bool scaled = kmax * c <= kScaledKeyMaxNorm && qmax <= kScaledKeyMaxNorm &&
+                        qmax * c * kmax <= scaled_key_bound<T>();
+    if (scaled != SCALED) return;
+    if constexpr (SCALED) {
+      kb = reinterpret_cast<const T*>(p.kc) + (int64_t)bh * p.key_tiles * kBlockN * kHeadDim;
+      kss = kHeadDim;
+    }
+  }
+
+  if constexpr (SCALED && !std::is_same<T, f16>::value) {
+    // Q in fp16 (kept in the same registers): exact for |q| <= 4096 down to
+    // the fp16 normal range.
+#pragma unroll
+    for (int g = 0; g < QG; ++g)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        f16x8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (f16)(float)qop[g][s][e];
+        qop[g][s] = __builtin_bit_cast(V8, h);
+      }
+  }
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
   float kn_next = bounded ? knorm[0] : 0.0f;
 
   for (int j = 0; j < n_tiles; ++j) {
@@ -336,7 +422,8 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     const int k0 = j * kBlockN;
 
     if (k0 <= wq_last) {  // wave-uniform: skip tiles entirely above this wave's rows
-      // S^T[key][query] for 2 subtiles of 32 keys.
+      // S^T[key][query] for 2 subtiles of 32 keys; on the scaled-key path
+      // both operands hold fp16 bits and the result is c q.k.
       f32x16 sacc[QG][2];
 #pragma unroll
       for (int g = 0; g < QG; ++g)
@@ -351,7 +438,12 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
           const V8 a = *reinterpret_cast<const V8*>(
               &k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
 #pragma unroll
-          for (int g = 0; g < QG; ++g) sacc[g][t] = mfma32(a, qop[g][s], sacc[g][t]);
+          for (int g = 0; g < QG; ++g)
+            if constexpr (SCALED)
+              sacc[g][t] = mfma32(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, qop[g][s]),
+                                  sacc[g][t]);
+            else
+              sacc[g][t] = mfma32(a, qop[g][s], sacc[g][t]);
         }
       }
 
@@ -373,50 +465,68 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       V8 pb[QG][4];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
-        // Rows whose bound keeps every probability below 2^safe_exponent skip the
-        // tile maximum.  Rows that need it move their shift up to the tile
-        // maximum only when that exceeds it by more than kLazyShift (log2
-        // units), so the O rescale is rare.  Both decisions are per row, so
-        // results do not depend on the launch.
-        const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
-        if (__any(need)) {
-        float mx = sacc[g][0][0];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
-        mx = half_swap_max(mx);
-        const bool grow = need && (mx - m_run[g]) * c > kLazyShift;
-        if (__any(grow)) {
-          const float m_new = grow ? mx : m_run[g];
-          const float alpha = exp2f((m_run[g] - m_new) * c);
-          l_run[g] *= alpha;
-#pragma unroll
-          for (int d = 0; d < 2; ++d)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
-          m_run[g] = m_new;
-        }
-        }
-        const float mc = m_run[g] * c;
         float lsum = l_run[g];
+        if constexpr (SCALED) {
+          // P = exp2(c q.k): every score lies within the bound, no shift.
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int t = u >> 1;
-          const int rb = (u & 1) * 8;
-          V8 pk;
+          for (int u = 0; u < 4; ++u) {
+            const int t = u >> 1;
+            const int rb = (u & 1) * 8;
+            V8 pk;
 #pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e], c, -mc));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e + 1], c, -mc));
-            V2 pair;
-            pair[0] = (T)p0;
-            pair[1] = (T)p1;
-            lsum = dot2_sum(pair, lsum);
-            pk[e] = pair[0];
-            pk[e + 1] = pair[1];
+            for (int e = 0; e < 8; e += 2) {
+              V2 pair;
+              pair[0] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e]);
+              pair[1] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e + 1]);
+              lsum = dot2_sum(pair, lsum);
+              pk[e] = pair[0];
+              pk[e + 1] = pair[1];
+            }
+            pb[g][u] = pk;
           }
-          pb[g][u] = pk;
+        } else {
+          // Rows whose bound keeps every probability below 2^safe_exponent skip the
+          // tile maximum.  Rows that need it move their shift up to the tile
+          // maximum only when that exceeds it by more than kLazyShift (log2
+          // units), so the O rescale is rare.  Both decisions are per row, so
+          // results do not depend on the launch.
+          const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
+          if (__any(need)) {
+            float mx = sacc[g][0][0];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
+            mx = half_swap_max(mx);
+            const bool grow = need && (mx - m_run[g]) * c > kLazyShift;
+            if (__any(grow)) {
+              const float m_new = grow ? mx : m_run[g];
+              const float alpha = exp2f((m_run[g] - m_new) * c);
+              lsum *= alpha;
+#pragma unroll
+              for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
+              m_run[g] = m_new;
+            }
+          }
+          const float mc = m_run[g] * c;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int t = u >> 1;
+            const int rb = (u & 1) * 8;
+            V8 pk;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+              V2 pair;
+              pair[0] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e], c, -mc));
+              pair[1] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e + 1], c, -mc));
+              lsum = dot2_sum(pair, lsum);
+              pk[e] = pair[0];
+              pk[e + 1] = pair[1];
+            }
+            pb[g][u] = pk;
+          }
         }
         l_run[g] = lsum;
       }
@@ -943,12 +1053,18 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnF32Params p) {
   }
 }
 
-// Largest |k| of every 64-key tile of every (batch, head): one wavefront per
-// tile, one key per lane (64 head-dim elements, fp32 sum of squares).
+// Largest |k| of every 64-row tile of every (batch, head) of k (keys, or the
+// queries for their table) and, with kc non-null, every row times c rounded
+// to fp16 ([batch*heads][key_tiles * 64][64]; rows past the sequence are not
+// written).  zero: write 0 norms (queries of a zero scale, which the
+// attention reads as zero).  One wavefront per tile, eight lanes per row with
+// 16 bytes each, so the reads and the fp16 writes are contiguous runs; fp32
+// sums of squares.
 template <typename T>
 __global__ __launch_bounds__(256) void key_norm_kernel(
-    const T* __restrict__ k, float* __restrict__ out, int64_t k_sb, int64_t k_sh,
-    int64_t k_ss, int heads, int seq_len, int key_tiles, int64_t total_tiles) {
+    const T* __restrict__ k, float* __restrict__ out, f16* __restrict__ kc, float c, int zero,
+    int64_t k_sb, int64_t k_sh, int64_t k_ss, int heads, int seq_len, int key_tiles,
+    int64_t total_tiles) {
   const int64_t tile_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tile_id >= total_tiles) return;  // wave-uniform
   const int lane = threadIdx.x & 63;
@@ -956,21 +1072,34 @@ __global__ __launch_bounds__(256) void key_norm_kernel(
   const int tile = (int)(tile_id - (int64_t)bh * key_tiles);
   const int b = bh / heads;
   const int h = bh - b * heads;
-  const int key = tile * 64 + lane;
-  float ss = 0.0f;
-  if (key < seq_len) {
-    const T* row = k + b * k_sb + h * k_sh + (int64_t)key * k_ss;
+  const T* base = k + b * k_sb + h * k_sh;
+  const int c8 = (lane & 7) * 8;
+  float mx = 0.0f;
 #pragma unroll
-    for (int c8 = 0; c8 < kHeadDim; c8 += 8) {
+  for (int i = 0; i < 8; ++i) {
+    const int key = tile * 64 + 8 * i + (lane >> 3);
+    float ss = 0.0f;
+    if (key < seq_len) {
       float f[8];
-      unpack8<T>(load16(row + c8), f);
+      unpack8<T>(load16(base + (int64_t)key * k_ss + c8), f);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+      if (kc != nullptr) {
+        f16x8 scaled;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) scaled[e] = (f16)fp32_result<f16>(f[e] * c);  // fp32 product, then fp16
+        store16(kc + ((int64_t)bh * key_tiles * 64 + key) * kHeadDim + c8,
+                __builtin_bit_cast(u32x4, scaled));
+      }
     }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    mx = fmaxf(mx, ss);
   }
 #pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) ss = fmaxf(ss, __shfl_xor(ss, offset));
-  if (lane == 0) out[tile_id] = sqrtf(ss);
+  for (int offset = 32; offset >= 8; offset >>= 1) mx = fmaxf(mx, __shfl_xor(mx, offset));
+  if (lane == 0) out[tile_id] = zero ? 0.0f : sqrtf(mx);
 }
 
 // [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
@@ -1024,13 +1153,20 @@ bool launch_supported(int block_m, int block_n, int num_warps, int num_stages) {
   return block_m == 32 * num_warps || block_m == 64 * num_warps;
 }
 
-template <typename T, int WAVES>
+template <typename T, int WAVES, int PATH>
 const void* plain_kernel(int qg, int num_stages) {
   if (qg == 1)
-    return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 2, WAVES>)
-                           : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 1, WAVES>);
-  return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 2, WAVES>)
-                         : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 1, WAVES>);
+    return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 2, WAVES, PATH>)
+                           : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 1, 1, WAVES, PATH>);
+  return num_stages == 2 ? reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 2, WAVES, PATH>)
+                         : reinterpret_cast<const void*>(&attn_fwd_kernel<T, 2, 1, WAVES, PATH>);
+}
+
+template <typename T, int WAVES>
+const void* plain_kernel_path(int qg, int num_stages, int path) {
+  if (path == kPathScaled) return plain_kernel<T, WAVES, kPathScaled>(qg, num_stages);
+  if (path == kPathShifted) return plain_kernel<T, WAVES, kPathShifted>(qg, num_stages);
+  return plain_kernel<T, WAVES, kPathAll>(qg, num_stages);
 }
 
 // Workgroups of `kernel` that fit on one CU at once (registers, LDS, waves),
@@ -1094,7 +1230,23 @@ int launch_attention(AttnParams prm, int block_m, int num_warps, int num_stages,
     threads = kThreads;
   } else {
     const int qg = block_m / (32 * num_warps);
-    kernel = num_warps == 8 ? plain_kernel<T, 8>(qg, num_stages) : plain_kernel<T, 4>(qg, num_stages);
+    if (prm.kc != nullptr) {
+      // The scaled-key workgroups, then the others, over the same grid.
+      threads = num_warps * 64;
+      for (int path : {kPathScaled, kPathShifted}) {
+        kernel = num_warps == 8 ? plain_kernel_path<T, 8>(qg, num_stages, path)
+                                : plain_kernel_path<T, 4>(qg, num_stages, path);
+        prm.head_group = head_group_for(batch_heads, prm.num_q_tiles, kernel, threads);
+        void* args[] = {&prm};
+        const int status =
+            check_hip(hipLaunchKernel(kernel, dim3(prm.num_blocks), dim3(threads), args, 0, stream),
+                      "attention kernel launch");
+        if (status != SAH_OK) return status;
+      }
+      return SAH_OK;
+    }
+    kernel = num_warps == 8 ? plain_kernel_path<T, 8>(qg, num_stages, kPathAll)
+                            : plain_kernel_path<T, 4>(qg, num_stages, kPathAll);
     threads = num_warps * 64;
   }
   prm.head_group = head_group_for(batch_heads, prm.num_q_tiles, kernel, threads);
@@ -1116,13 +1268,14 @@ int launch_transpose(const void* v, void* vt, int64_t batch, int64_t heads,
 }
 
 template <typename T>
-int launch_key_norm(const void* k, float* out, int64_t batch, int64_t heads, int64_t seq_len,
-                    int64_t k_sb, int64_t k_sh, int64_t k_ss, hipStream_t stream) {
+int launch_key_norm(const void* k, float* out, f16* kc, float c, bool zero, int64_t batch,
+                    int64_t heads, int64_t seq_len, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                    hipStream_t stream) {
   const int64_t key_tiles = ceil_div(seq_len, 64);
   const int64_t total = batch * heads * key_tiles;
   hipLaunchKernelGGL((key_norm_kernel<T>), dim3((unsigned)ceil_div(total, 4)), dim3(256), 0,
-                     stream, static_cast<const T*>(k), out, k_sb, k_sh, k_ss, (int)heads,
-                     (int)seq_len, (int)key_tiles, total);
+                     stream, static_cast<const T*>(k), out, kc, c, zero ? 1 : 0, k_sb, k_sh, k_ss,
+                     (int)heads, (int)seq_len, (int)key_tiles, total);
   return check_hip(hipGetLastError(), "key norm launch");
 }
 
@@ -1131,6 +1284,13 @@ int launch_key_norm(const void* k, float* out, int64_t batch, int64_t heads, int
 size_t key_norm_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
   if (seq_len < kKeyNormMinSeq) return 0;
   return (size_t)ceil_div(batch * heads * ceil_div(seq_len, 64) * (int64_t)sizeof(float), 256) * 256;
+}
+
+// Bytes of the scaled fp16 keys that go with the table (64-key tiles of 64
+// elements); 0 for sequences that run without it.
+size_t scaled_key_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
+  if (seq_len < kKeyNormMinSeq) return 0;
+  return (size_t)batch * (size_t)heads * (size_t)padded_seq(seq_len) * kHeadDim * sizeof(f16);
 }
 
 }  // namespace
@@ -1151,9 +1311,10 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
   (void)v_stride_s;
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
   if (dtype == SAH_DTYPE_F32) return 0;  // the fp32 kernel reads K and V as given
-  const size_t norms = key_norm_bytes(batch, heads, seq_len);
-  if (v_stride_d != 1) return norms;  // V already seq-contiguous (V^T storage)
-  return norms + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
+  const size_t table =
+      2 * key_norm_bytes(batch, heads, seq_len) + scaled_key_bytes(batch, heads, seq_len);
+  if (v_stride_d != 1) return table;  // V already seq-contiguous (V^T storage)
+  return table + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
 }
 
 extern "C" int sah_causal_attention_bsd(
@@ -1270,8 +1431,8 @@ extern "C" int sah_causal_attention_bsd(
   prm.num_q_tiles = (int)q_tiles;
   prm.num_blocks = (int)blocks;
 
-  // Workspace: the per-tile key-norm table (long sequences), then (reference
-  // V layout only) V^T.
+  // Workspace: the per-tile key-norm and query-norm tables and the fp16
+  // scaled keys (long sequences), then (reference V layout only) V^T.
   const size_t need = sah_causal_attention_workspace_bytes(
       batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -1280,21 +1441,39 @@ extern "C" int sah_causal_attention_bsd(
   if (need > 0 && !aligned16(workspace))
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention workspace must be 16-byte aligned");
   const size_t norm_bytes = key_norm_bytes(batch, heads, seq_len);
-  void* vt_space = need > 0 ? static_cast<unsigned char*>(workspace) + norm_bytes : nullptr;
+  const size_t kc_bytes = scaled_key_bytes(batch, heads, seq_len);
+  void* vt_space =
+      need > 0 ? static_cast<unsigned char*>(workspace) + 2 * norm_bytes + kc_bytes : nullptr;
   int status = SAH_OK;
   prm.knorm = nullptr;
+  prm.qnorm = nullptr;
+  prm.kc = nullptr;
   prm.key_tiles = (int)ceil_div(seq_len, 64);
   // The pipelined kernel (num_stages 3) keeps the exact running maximum and
-  // never reads the table; its region of the workspace then stays unused.
+  // never reads the table; its regions of the workspace then stay unused.
   if (norm_bytes > 0 && num_stages != 3) {
-    float* norms = static_cast<float*>(workspace);
-    status = (dtype == SAH_DTYPE_BF16)
-                 ? launch_key_norm<bf16>(key, norms, batch, heads, seq_len, k_stride_b,
-                                         k_stride_h, k_stride_s, stream)
-                 : launch_key_norm<f16>(key, norms, batch, heads, seq_len, k_stride_b,
-                                        k_stride_h, k_stride_s, stream);
+    unsigned char* base = static_cast<unsigned char*>(workspace);
+    float* norms = reinterpret_cast<float*>(base);
+    float* qnorms = reinterpret_cast<float*>(base + norm_bytes);
+    f16* kc = reinterpret_cast<f16*>(base + 2 * norm_bytes);
+    const bool zero_q = prm.q_and == 0u;
+    if (dtype == SAH_DTYPE_BF16) {
+      status = launch_key_norm<bf16>(key, norms, kc, prm.c, false, batch, heads, seq_len,
+                                     k_stride_b, k_stride_h, k_stride_s, stream);
+      if (status == SAH_OK)
+        status = launch_key_norm<bf16>(query, qnorms, nullptr, prm.c, zero_q, batch, heads,
+                                       seq_len, q_stride_b, q_stride_h, q_stride_s, stream);
+    } else {
+      status = launch_key_norm<f16>(key, norms, kc, prm.c, false, batch, heads, seq_len,
+                                    k_stride_b, k_stride_h, k_stride_s, stream);
+      if (status == SAH_OK)
+        status = launch_key_norm<f16>(query, qnorms, nullptr, prm.c, zero_q, batch, heads,
+                                      seq_len, q_stride_b, q_stride_h, q_stride_s, stream);
+    }
     if (status != SAH_OK) return status;
     prm.knorm = norms;
+    prm.qnorm = qnorms;
+    prm.kc = kc;
   }
   if (v_stride_d == 1) {
     // Reference layout: transpose V into the workspace first.

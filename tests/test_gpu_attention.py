@@ -309,6 +309,76 @@ def test_fp16_score_bound_keeps_probabilities_in_range(gpu_device):
         _assert_parity(torch.from_numpy(expected).float(), actual, torch.float16, f"fp16 head {head}")
 
 
+@pytest.mark.parametrize("dtype,magnitude", [(torch.bfloat16, 1.0), (torch.float16, 0.5)])
+def test_scaled_key_path_sampled_rows(gpu_device, dtype, magnitude):
+    """S = 20000 with moderate scores: every workgroup's bound c |q| max|k|
+    is within the scaled-key limit (32 for bf16 P, 15 for fp16 P), so the
+    scores come from the fp16 MFMA on the pre-pass's scaled keys and P =
+    exp2(score) without a shift.  Sampled rows against float64 per-row math,
+    and the 8-wave and 4-wave launches bitwise equal."""
+
+    seq = 20_000
+    print(f"scaled-key attention S={seq} {dtype} x{magnitude}", flush=True)
+    q, k, v = _inputs(1, 2, seq, dtype=dtype, seed=91, scale_inputs=magnitude)
+    outputs = [
+        _run(q, k, v, gpu_device, block_m=block_m, num_warps=warps, num_stages=2).float().cpu()
+        for block_m, warps in ((256, 8), (128, 4))
+    ]
+    assert torch.equal(outputs[0], outputs[1])
+    rng = np.random.default_rng(3)
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.arange(seq - 20, seq), rng.integers(0, seq, 60)]))
+    for head in range(2):
+        expected = causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(),
+            rows, 1 / 8,
+        )
+        actual = outputs[0][0, rows, head * 64 : (head + 1) * 64]
+        _assert_parity(torch.from_numpy(expected).float(), actual, dtype, f"scaled keys head {head}")
+
+
+def test_scaled_keys_in_the_workspace(gpu_device):
+    """The pre-pass writes the largest |k| and the largest |q| of every 64-row
+    tile into two tables, then every key times c = scale * log2(e) rounded to
+    fp16 as [batch*heads][key_tiles * 64][64]."""
+
+    from solution.kernels.hip._library import load_library
+
+    batch, heads, seq = 1, 3, 16_500
+    q, k, v = _inputs(batch, heads, seq, dtype=torch.bfloat16, seed=12)
+    library = load_library()
+    vt = torch.zeros(batch, heads, 64, -(-seq // 64) * 64, dtype=torch.bfloat16)
+    vt[..., :seq] = v.transpose(-2, -1)
+    qd, kd, vtd = q.to(gpu_device), k.to(gpu_device), vt.to(gpu_device)
+    value = vtd[..., :seq].transpose(-2, -1)
+    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 1, value.stride(3), 2)
+    tiles = -(-seq // 64)
+    table = -(-(batch * heads * tiles * 4) // 256) * 256
+    assert need == 2 * table + batch * heads * tiles * 64 * 64 * 2
+    workspace = torch.zeros(need, dtype=torch.uint8, device=gpu_device)
+    out = torch.empty(batch, seq, heads * 64, dtype=torch.bfloat16, device=gpu_device)
+    scale = 0.125
+    status = library.sah_causal_attention_bsd(
+        qd.data_ptr(), kd.data_ptr(), value.data_ptr(), out.data_ptr(), batch, heads, seq, 64,
+        *qd.stride()[:3], *kd.stride()[:3], *value.stride(), out.stride(0), out.stride(1),
+        scale, 2, 256, 64, 8, 2, workspace.data_ptr(), need, torch.cuda.current_stream().cuda_stream,
+    )
+    assert status == 0
+    torch.cuda.synchronize()
+    host = workspace.cpu()
+    norms = host[: batch * heads * tiles * 4].view(torch.float32).view(batch * heads, tiles)
+    padded = torch.zeros(batch * heads, tiles * 64, 64)
+    padded[:, :seq] = k.float().reshape(batch * heads, seq, 64)
+    want_norms = padded.norm(dim=-1).view(batch * heads, tiles, 64).amax(-1)
+    assert torch.allclose(norms, want_norms, rtol=1e-5, atol=0)
+    qnorms = host[table : table + batch * heads * tiles * 4].view(torch.float32).view(batch * heads, tiles)
+    padded[:, :seq] = q.float().reshape(batch * heads, seq, 64)
+    want_qnorms = padded.norm(dim=-1).view(batch * heads, tiles, 64).amax(-1)
+    assert torch.allclose(qnorms, want_qnorms, rtol=1e-5, atol=0)
+    scaled = host[2 * table :].view(torch.float16).view(batch * heads, tiles * 64, 64)[:, :seq]
+    want = (k.float().reshape(batch * heads, seq, 64) * np.float32(scale * math.log2(math.e))).half()
+    assert torch.equal(scaled, want)
+
+
 def test_invalid_launch_and_ineligible_inputs_raise(gpu_device):
     module = _attention_module()
     q, k, v = (t.to(gpu_device) for t in _inputs(1, 1, 64, dtype=torch.bfloat16, seed=1))
@@ -358,6 +428,28 @@ def test_negative_scale_matches_oracle_and_negated_query(gpu_device, block_m, nu
     _assert_parity(_to_bsd(_oracle(q, k, v, scale)), output, torch.bfloat16, f"scale {scale}")
     flipped = _run(-q, k, v, gpu_device, scale=-scale, **launch)
     assert torch.equal(output, flipped)
+
+
+def test_negative_scale_on_the_scaled_key_path(gpu_device):
+    """S = 16500 (key-norm pre-pass, scaled keys): a negative scale folds its
+    sign into the query, so it equals the positive scale on the negated query
+    bitwise, and sampled rows match float64."""
+
+    seq = 16_500
+    print(f"negative scale scaled-key path S={seq}", flush=True)
+    q, k, v = _inputs(1, 2, seq, dtype=torch.bfloat16, seed=23)
+    launch = dict(block_m=256, num_warps=8, num_stages=2)
+    output = _run(q, k, v, gpu_device, scale=-1 / 8, **launch)
+    flipped = _run(-q, k, v, gpu_device, scale=1 / 8, **launch)
+    assert torch.equal(output, flipped)
+    rows = np.unique(np.concatenate([np.arange(0, 10), np.arange(seq - 10, seq), np.arange(8000, 8040)]))
+    for head in range(2):
+        expected = causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(),
+            rows, -1 / 8,
+        )
+        actual = output.float().cpu()[0, rows, head * 64 : (head + 1) * 64]
+        _assert_parity(torch.from_numpy(expected).float(), actual, torch.bfloat16, f"negative scale head {head}")
 
 
 @pytest.mark.parametrize("block_m,num_warps,num_stages", [(128, 4, 2), (256, 8, 2)])
