@@ -64,6 +64,8 @@ attention at B8 H16 S2048 Dh64 under every implemented launch, with V in
 [B, H, S, 64] and in seq-contiguous layout, or the fused residual +
 LayerNorm on [16384, 1024] under a few launches; each line is the mean of
 ``--repeat`` back-to-back launches.
+``--resident c2|c4`` runs one resident configuration's latency protocol alone
+and prints its JSON summary (for a kernel-trace profile of that forward).
 """
 
 from __future__ import annotations
@@ -773,6 +775,10 @@ def _percentile(values, q):
     return ordered[lower] + (ordered[upper] - ordered[lower]) * (position - lower)
 
 
+# The headline's resident configurations C2 and C4 as (B, S, D, H, F, L), bf16.
+RESIDENT_SHAPES = {"c2": (64, 256, 512, 8, 2048, 4), "c4": (16, 4096, 2048, 32, 8192, 2)}
+
+
 def resident_latency(shape: tuple, *, warmup: int = 20, repeats: int = 100, rounds: int = 3) -> dict:
     """GPU forward latency of a resident configuration under the reference's
     formal protocol (benchmarking/protocols.py:116-117: 20 warm-up calls,
@@ -899,6 +905,8 @@ def main() -> int:
                                              "boundary-ffn-torch", "attention-c3", "norm-c3"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
+    parser.add_argument("--resident", choices=tuple(RESIDENT_SHAPES),
+                        help="time one resident configuration's forward alone (profiling)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(
@@ -914,6 +922,9 @@ def main() -> int:
         return config3_alone(args.kernel, max(1, args.repeat))
     if args.kernel is not None:
         return kernel_alone(args.kernel, max(1, args.repeat))
+    if args.resident is not None:
+        print(json.dumps(resident_latency(RESIDENT_SHAPES[args.resident])), flush=True)
+        return 0
 
     # The operators alone first: directly after the forward the chip runs hot
     # and its clock is lower (attention 114 us there against ~102 us here).
@@ -921,8 +932,7 @@ def main() -> int:
     gpu = gpu_benchmark(args.steps, args.warmup, check=not args.no_check)
     resident = None
     if not args.no_resident:
-        resident = {"c2": resident_latency((64, 256, 512, 8, 2048, 4)),
-                    "c4": resident_latency((16, 4096, 2048, 32, 8192, 2))}
+        resident = {name: resident_latency(shape) for name, shape in RESIDENT_SHAPES.items()}
         log(f"resident: C2 {resident['c2']['median_ms']} ms, C4 {resident['c4']['median_ms']} ms (median)")
     threads, affinity, quota = _cpu_cores()
     baseline = None
