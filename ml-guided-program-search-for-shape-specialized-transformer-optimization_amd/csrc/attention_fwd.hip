@@ -270,6 +270,33 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   const int key_end = min(q0 + BM, S);
   const int n_tiles = (key_end + kBlockN - 1) / kBlockN;
 
+  // ---- scaled-key path: taken by the block of kScaledKeyRows query rows
+  // that holds this workgroup's rows when c max|q| max|k| <= scaled_key_bound
+  // over the block's rows and the keys they read (and both operands fit fp16
+  // comfortably).  Every wave forms the same exact maxima, so the workgroup
+  // returns as a whole or not at all, before it loads anything else.
+  constexpr bool SCALED = PATH == kPathScaled;
+  if constexpr (PATH != kPathAll) {  // the host launches these only with the tables
+    const int row0 = (q0 / kScaledKeyRows) * kScaledKeyRows;
+    const int block_tiles = (min(row0 + kScaledKeyRows, S) + kBlockN - 1) / kBlockN;
+    typedef const __attribute__((address_space(1))) float* TableFloats;
+    TableFloats knorm = (TableFloats)p.knorm + (int64_t)bh * p.key_tiles;
+    TableFloats qnorm = (TableFloats)p.qnorm + (int64_t)bh * p.key_tiles;
+    float kmax = 0.0f, qmax = 0.0f;
+    for (int t = lane; t < block_tiles; t += 64) kmax = fmaxf(kmax, knorm[t]);
+    for (int t = row0 / kBlockN + lane; t < block_tiles; t += 64) qmax = fmaxf(qmax, qnorm[t]);
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+      kmax = fmaxf(kmax, __shfl_xor(kmax, offset));
+      qmax = fmaxf(qmax, __shfl_xor(qmax, offset));
+    }
+    const float c = p.c;
+    const bool scaled = kmax * c <= kScaledKeyMaxNorm && qmax <= kScaledKeyMaxNorm &&
+                        qmax * c * kmax <= scaled_key_bound<T>();
+    if (scaled != SCALED) return;
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads below after the exit
+  }
+
   // ---- Q^T operands (B operand of S^T = K Q^T), kept in registers; the
   // sign fold of a non-positive scale is skipped (uniform branch) otherwise.
   const bool q_transform = p.q_and != 0xffffffffu || p.q_xor != 0u;
@@ -301,9 +328,10 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   }
 
   // Key source: the keys as given, or the pre-pass's fp16 keys times c on the
-  // scaled-key path (chosen below, before the first tile is staged).
-  const T* kb = kbase;
-  int64_t kss = p.k_ss;
+  // scaled-key path.
+  const T* kb = SCALED ? reinterpret_cast<const T*>(p.kc) + (int64_t)bh * p.key_tiles * kBlockN * kHeadDim
+                       : kbase;
+  const int64_t kss = SCALED ? (int64_t)kHeadDim : p.k_ss;
 
   // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
   u32x4 k_pref[CPT], v_pref[CPT];
@@ -366,33 +394,6 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   // of the loop also waited for (6% slower on the long-sequence chunk).
   typedef const __attribute__((address_space(1))) float* GlobalFloats;
   GlobalFloats knorm = bounded ? (GlobalFloats)p.knorm + (int64_t)bh * p.key_tiles : nullptr;
-
-  // ---- scaled-key path: taken by the block of kScaledKeyRows query rows
-  // that holds this workgroup's rows when c max|q| max|k| <= scaled_key_bound
-  // over the block's rows and the keys they read (and both operands fit fp16
-  // comfortably).  Every wave forms the same exact maxima, so the workgroup
-  // returns as a whole or not at all.
-  constexpr bool SCALED = PATH == kPathScaled;
-  if constexpr (PATH != kPathAll) {  // the host launches these only with the tables
-    const int row0 = (q0 / kScaledKeyRows) * kScaledKeyRows;
-    const int block_tiles = (min(row0 + kScaledKeyRows, S) + kBlockN - 1) / kBlockN;
-    GlobalFloats qnorm = (GlobalFloats)p.qnorm + (int64_t)bh * p.key_tiles;
-    float kmax = 0.0f, qmax = 0.0f;
-    for (int t = lane; t < block_tiles; t += 64) kmax = fmaxf(kmax, knorm[t]);
-    for (int t = row0 / kBlockN + lane; t < block_tiles; t += 64) qmax = fmaxf(qmax, qnorm[t]);
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-      kmax = fmaxf(kmax, __shfl_xor(kmax, offset));
-      qmax = fmaxf(qmax, __shfl_xor(qmax, offset));
-    }
-    const bool scaled = kmax * c <= kScaledKeyMaxNorm && qmax <= kScaledKeyMaxNorm &&
-                        qmax * c * kmax <= scaled_key_bound<T>();
-    if (scaled != SCALED) return;
-    if constexpr (SCALED) {
-      kb = reinterpret_cast<const T*>(p.kc) + (int64_t)bh * p.key_tiles * kBlockN * kHeadDim;
-      kss = kHeadDim;
-    }
-  }
 
   if constexpr (SCALED && !std::is_same<T, f16>::value) {
     // Q in fp16 (kept in the same registers): exact for |q| <= 4096 down to
