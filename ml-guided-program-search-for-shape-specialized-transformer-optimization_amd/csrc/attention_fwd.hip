@@ -449,17 +449,19 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       }
 
       // Causal mask: only tiles that reach past this wave's first query.
+      // Element r of subtile t is key k0 + 32 t + 16 (r / 8) + 8 half + r % 8;
+      // it is masked when that exceeds the lane's query, i.e. when the
+      // constant 32 t + 16 (r / 8) + r % 8 exceeds qi - k0 - 8 half (one
+      // compare against an immediate per element).
       if (k0 + kBlockN - 1 > wq0) {
 #pragma unroll
         for (int g = 0; g < QG; ++g) {
-          const int qi = wq0 + 32 * g + l32;
+          const int lim = wq0 + 32 * g + l32 - k0 - 8 * half;
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = k0 + 32 * t + 16 * (r >> 3) + 8 * half + (r & 7);
-              if (key > qi) sacc[g][t][r] = -INFINITY;
-            }
+            for (int r = 0; r < 16; ++r)
+              if (32 * t + 16 * (r >> 3) + (r & 7) > lim) sacc[g][t][r] = -INFINITY;
         }
       }
 
