@@ -99,7 +99,8 @@ int sah_causal_attention_bsd(
     sah_stream_t stream);
 
 /* Workspace bytes sah_causal_attention_bsd needs: for seq_len >= 16384 the
- * key-norm and query-norm tables (4 bytes per 64-row tile per head, each
+ * key-norm table (4 bytes per 64-key tile per head, rounded up to 256), the
+ * key and query block-norm tables (8 bytes per 512-row block per head,
  * rounded up to 256) and the fp16 scaled keys (128 bytes per key, seq_len
  * rounded up to 64, per head), then V^T when value is head_dim-contiguous;
  * 0 for a seq-contiguous value shorter than 16384 keys. */
@@ -120,7 +121,7 @@ size_t sah_causal_attention_workspace_bytes(
  * exceeds that returns SAH_ERR_WORKSPACE before any launch (for example V in
  * the reference [B, H, S, 64] layout needs B*H*64*roundup(S, 64)*2 bytes, so
  * B8 H16 S2048 fits and one 2 x 100000-token chunk does not; a seq-contiguous
- * V needs only the key-norm table).  All calls on one GPU share its array:
+ * V needs only the norm tables and the scaled keys).  All calls on one GPU share its array:
  * calls that may overlap on that GPU (different streams, or host threads)
  * race on it and must be serialized by the caller.  Nothing in it needs to
  * start at zero; every call writes what it reads.

@@ -126,7 +126,7 @@ struct AttnParams {
   float c;
   uint32_t q_and, q_xor;
   // Largest key norm of every 64-key tile, [batch*heads][key_tiles]
-  // (key_norm_kernel), for the plain kernel's score bound; null when the
+  // (long_prepare_kernel), for the plain kernel's score bound; null when the
   // host skips that pre-pass (short sequences), and then every tile forms
   // its row maximum.
   const float* knorm;
@@ -134,8 +134,11 @@ struct AttnParams {
   // Keys times c in fp16, [batch*heads][key_tiles * 64][64] (rows past the
   // sequence never read), written by the pre-pass; null without it.
   const f16* kc;
-  // Largest |q| of every 64-row tile, laid out as knorm; set with kc.
-  const float* qnorm;
+  // Largest |k| and largest |q| of every block of kScaledKeyRows rows,
+  // [batch*heads][num_row_blocks] each; set with kc.
+  const float* kblock;
+  const float* qblock;
+  int num_row_blocks;
 };
 
 // Workgroup id -> (batch*head, query tile).  With head_group G > 0, XCD x
@@ -277,19 +280,15 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   // returns as a whole or not at all, before it loads anything else.
   constexpr bool SCALED = PATH == kPathScaled;
   if constexpr (PATH != kPathAll) {  // the host launches these only with the tables
-    const int row0 = (q0 / kScaledKeyRows) * kScaledKeyRows;
-    const int block_tiles = (min(row0 + kScaledKeyRows, S) + kBlockN - 1) / kBlockN;
+    // The block's rows read keys [0, its end): key blocks 0 .. blk.
+    const int blk = q0 / kScaledKeyRows;
     typedef const __attribute__((address_space(1))) float* TableFloats;
-    TableFloats knorm = (TableFloats)p.knorm + (int64_t)bh * p.key_tiles;
-    TableFloats qnorm = (TableFloats)p.qnorm + (int64_t)bh * p.key_tiles;
-    float kmax = 0.0f, qmax = 0.0f;
-    for (int t = lane; t < block_tiles; t += 64) kmax = fmaxf(kmax, knorm[t]);
-    for (int t = row0 / kBlockN + lane; t < block_tiles; t += 64) qmax = fmaxf(qmax, qnorm[t]);
+    TableFloats kblock = (TableFloats)p.kblock + (int64_t)bh * p.num_row_blocks;
+    const float qmax = ((TableFloats)p.qblock)[(int64_t)bh * p.num_row_blocks + blk];
+    float kmax = 0.0f;
+    for (int t = lane; t <= blk; t += 64) kmax = fmaxf(kmax, kblock[t]);
 #pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-      kmax = fmaxf(kmax, __shfl_xor(kmax, offset));
-      qmax = fmaxf(qmax, __shfl_xor(qmax, offset));
-    }
+    for (int offset = 32; offset > 0; offset >>= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, offset));
     const float c = p.c;
     const bool scaled = kmax * c <= kScaledKeyMaxNorm && qmax <= kScaledKeyMaxNorm &&
                         qmax * c * kmax <= scaled_key_bound<T>();
@@ -1056,53 +1055,141 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnF32Params p) {
   }
 }
 
-// Largest |k| of every 64-row tile of every (batch, head) of k (keys, or the
-// queries for their table) and, with kc non-null, every row times c rounded
-// to fp16 ([batch*heads][key_tiles * 64][64]; rows past the sequence are not
-// written).  zero: write 0 norms (queries of a zero scale, which the
-// attention reads as zero).  One wavefront per tile, eight lanes per row with
-// 16 bytes each, so the reads and the fp16 writes are contiguous runs; fp32
-// sums of squares.
+// Long-sequence preparation of one block of kScaledKeyRows rows of one
+// (batch, head), one launch for the whole attention call:
+//  * K: the largest |k| of every 64-key tile (knorm) and of the block
+//    (kblock), and every key times c rounded to fp16 (kc, [batch*heads]
+//    [key_tiles * 64][64]; rows past the sequence are not written);
+//  * Q: the largest |q| of the block (qblock; 0 when zero_q: the queries of a
+//    zero scale, which the attention reads as zero);
+//  * V (vt non-null): V^T tiles [batch*heads][64][seq_pad], zero-filled for
+//    keys in [S, seq_pad).
+// Wave w takes tiles 2w and 2w + 1 of the block for K and Q: eight lanes per
+// row with 16 bytes each, so reads and fp16 writes are contiguous runs; fp32
+// sums of squares.  The V^T tiles go through LDS with all 256 threads.
+struct PrepParams {
+  const void* k;
+  const void* q;
+  const void* v;
+  float* knorm;
+  float* kblock;
+  float* qblock;
+  f16* kc;
+  void* vt;
+  int64_t k_sb, k_sh, k_ss, q_sb, q_sh, q_ss, v_sb, v_sh, v_ss;
+  int64_t seq_pad;
+  float c;
+  int zero_q;
+  int heads, seq_len, key_tiles, num_row_blocks;
+};
+
+// Largest |row| of 64-row tile `tile` of a [S, 64] matrix with row stride
+// `ss` (squared, fp32, in every lane); with kc non-null the tile's rows times
+// c are written there in fp16.
 template <typename T>
-__global__ __launch_bounds__(256) void key_norm_kernel(
-    const T* __restrict__ k, float* __restrict__ out, f16* __restrict__ kc, float c, int zero,
-    int64_t k_sb, int64_t k_sh, int64_t k_ss, int heads, int seq_len, int key_tiles,
-    int64_t total_tiles) {
-  const int64_t tile_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile_id >= total_tiles) return;  // wave-uniform
-  const int lane = threadIdx.x & 63;
-  const int bh = (int)(tile_id / key_tiles);
-  const int tile = (int)(tile_id - (int64_t)bh * key_tiles);
-  const int b = bh / heads;
-  const int h = bh - b * heads;
-  const T* base = k + b * k_sb + h * k_sh;
+__device__ __forceinline__ float tile_max_sq(const T* base, int64_t ss, int tile, int seq_len,
+                                             f16* kc, float c, int lane) {
   const int c8 = (lane & 7) * 8;
   float mx = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int key = tile * 64 + 8 * i + (lane >> 3);
-    float ss = 0.0f;
-    if (key < seq_len) {
+    const int row = tile * 64 + 8 * i + (lane >> 3);
+    float ss2 = 0.0f;
+    if (row < seq_len) {
       float f[8];
-      unpack8<T>(load16(base + (int64_t)key * k_ss + c8), f);
+      unpack8<T>(load16(base + (int64_t)row * ss + c8), f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+      for (int e = 0; e < 8; ++e) ss2 = fmaf(f[e], f[e], ss2);
       if (kc != nullptr) {
         f16x8 scaled;
 #pragma unroll
         for (int e = 0; e < 8; ++e) scaled[e] = (f16)fp32_result<f16>(f[e] * c);  // fp32 product, then fp16
-        store16(kc + ((int64_t)bh * key_tiles * 64 + key) * kHeadDim + c8,
-                __builtin_bit_cast(u32x4, scaled));
+        store16(kc + (int64_t)row * kHeadDim + c8, __builtin_bit_cast(u32x4, scaled));
       }
     }
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    ss += __shfl_xor(ss, 4);
-    mx = fmaxf(mx, ss);
+    ss2 += __shfl_xor(ss2, 1);
+    ss2 += __shfl_xor(ss2, 2);
+    ss2 += __shfl_xor(ss2, 4);
+    mx = fmaxf(mx, ss2);
   }
 #pragma unroll
   for (int offset = 32; offset >= 8; offset >>= 1) mx = fmaxf(mx, __shfl_xor(mx, offset));
-  if (lane == 0) out[tile_id] = zero ? 0.0f : sqrtf(mx);
+  return mx;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void long_prepare_kernel(PrepParams pp) {
+  __shared__ float red[2][4];
+  __shared__ T tile[64][kHeadDim + 2];
+  const int blk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / pp.heads;
+  const int h = bh - b * pp.heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int kTilesPerBlock = kScaledKeyRows / 64;
+  const int t0 = blk * kTilesPerBlock;
+  const int t_end = min(t0 + kTilesPerBlock, pp.key_tiles);
+
+  const T* kbase = static_cast<const T*>(pp.k) + b * pp.k_sb + h * pp.k_sh;
+  const T* qbase = static_cast<const T*>(pp.q) + b * pp.q_sb + h * pp.q_sh;
+  f16* kc = pp.kc + (int64_t)bh * pp.key_tiles * 64 * kHeadDim;
+  float kmax = 0.0f, qmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = t0 + 2 * wave + i;
+    if (t < t_end) {  // wave-uniform
+      const float km = tile_max_sq<T>(kbase, pp.k_ss, t, pp.seq_len, kc, pp.c, lane);
+      const float qm = tile_max_sq<T>(qbase, pp.q_ss, t, pp.seq_len, nullptr, 0.0f, lane);
+      if (lane == 0) pp.knorm[(int64_t)bh * pp.key_tiles + t] = sqrtf(km);
+      kmax = fmaxf(kmax, km);
+      qmax = fmaxf(qmax, qm);
+    }
+  }
+  if (lane == 0) {
+    red[0][wave] = kmax;
+    red[1][wave] = qmax;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float k4 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float q4 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    pp.kblock[(int64_t)bh * pp.num_row_blocks + blk] = sqrtf(k4);
+    pp.qblock[(int64_t)bh * pp.num_row_blocks + blk] = pp.zero_q ? 0.0f : sqrtf(q4);
+  }
+
+  if (pp.vt == nullptr) return;  // uniform
+  typedef typename Vec8<T>::type V8;
+  const T* vbase = static_cast<const T*>(pp.v) + b * pp.v_sb + h * pp.v_sh;
+  T* dst = static_cast<T*>(pp.vt) + (int64_t)bh * kHeadDim * pp.seq_pad;
+  for (int t = t0; t < t_end; ++t) {
+    const int k0 = t * 64;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + 256 * i;
+      const int row = chunk >> 3;
+      const int c8 = (chunk & 7) * 8;
+      const int key = k0 + row;
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (key < pp.seq_len) raw = load16(vbase + (int64_t)key * pp.v_ss + c8);
+      const V8 vals = __builtin_bit_cast(V8, raw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tile[row][c8 + e] = vals[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int chunk = tid + 256 * i;
+      const int d = chunk >> 3;
+      const int c8 = (chunk & 7) * 8;
+      V8 vals;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vals[e] = tile[c8 + e][d];
+      store16(dst + (int64_t)d * pp.seq_pad + k0 + c8, __builtin_bit_cast(u32x4, vals));
+    }
+    __syncthreads();  // the tile is rewritten for the next 64 keys
+  }
 }
 
 // [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
@@ -1271,15 +1358,10 @@ int launch_transpose(const void* v, void* vt, int64_t batch, int64_t heads,
 }
 
 template <typename T>
-int launch_key_norm(const void* k, float* out, f16* kc, float c, bool zero, int64_t batch,
-                    int64_t heads, int64_t seq_len, int64_t k_sb, int64_t k_sh, int64_t k_ss,
-                    hipStream_t stream) {
-  const int64_t key_tiles = ceil_div(seq_len, 64);
-  const int64_t total = batch * heads * key_tiles;
-  hipLaunchKernelGGL((key_norm_kernel<T>), dim3((unsigned)ceil_div(total, 4)), dim3(256), 0,
-                     stream, static_cast<const T*>(k), out, kc, c, zero ? 1 : 0, k_sb, k_sh, k_ss,
-                     (int)heads, (int)seq_len, (int)key_tiles, total);
-  return check_hip(hipGetLastError(), "key norm launch");
+int launch_long_prepare(const PrepParams& pp, int64_t batch_heads, hipStream_t stream) {
+  const dim3 grid((unsigned)pp.num_row_blocks, (unsigned)batch_heads), block(256);
+  hipLaunchKernelGGL((long_prepare_kernel<T>), grid, block, 0, stream, pp);
+  return check_hip(hipGetLastError(), "long-sequence preparation launch");
 }
 
 // Bytes of the per-tile key-norm table, rounded up to 256; 0 for sequences
@@ -1287,6 +1369,13 @@ int launch_key_norm(const void* k, float* out, f16* kc, float c, bool zero, int6
 size_t key_norm_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
   if (seq_len < kKeyNormMinSeq) return 0;
   return (size_t)ceil_div(batch * heads * ceil_div(seq_len, 64) * (int64_t)sizeof(float), 256) * 256;
+}
+
+// Bytes of the two per-block tables (largest |k|, largest |q| of every block
+// of kScaledKeyRows rows), rounded up to 256; 0 without the key-norm table.
+size_t row_block_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
+  if (seq_len < kKeyNormMinSeq) return 0;
+  return (size_t)ceil_div(2 * batch * heads * ceil_div(seq_len, kScaledKeyRows) * (int64_t)sizeof(float), 256) * 256;
 }
 
 // Bytes of the scaled fp16 keys that go with the table (64-key tiles of 64
@@ -1314,8 +1403,9 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
   (void)v_stride_s;
   if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
   if (dtype == SAH_DTYPE_F32) return 0;  // the fp32 kernel reads K and V as given
-  const size_t table =
-      2 * key_norm_bytes(batch, heads, seq_len) + scaled_key_bytes(batch, heads, seq_len);
+  const size_t table = key_norm_bytes(batch, heads, seq_len) +
+                       row_block_bytes(batch, heads, seq_len) +
+                       scaled_key_bytes(batch, heads, seq_len);
   if (v_stride_d != 1) return table;  // V already seq-contiguous (V^T storage)
   return table + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
 }
@@ -1434,8 +1524,9 @@ extern "C" int sah_causal_attention_bsd(
   prm.num_q_tiles = (int)q_tiles;
   prm.num_blocks = (int)blocks;
 
-  // Workspace: the per-tile key-norm and query-norm tables and the fp16
-  // scaled keys (long sequences), then (reference V layout only) V^T.
+  // Workspace: the per-tile key-norm table, the per-block key and query norm
+  // tables and the fp16 scaled keys (long sequences), then (reference V
+  // layout only) V^T.
   const size_t need = sah_causal_attention_workspace_bytes(
       batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
@@ -1444,67 +1535,89 @@ extern "C" int sah_causal_attention_bsd(
   if (need > 0 && !aligned16(workspace))
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention workspace must be 16-byte aligned");
   const size_t norm_bytes = key_norm_bytes(batch, heads, seq_len);
+  const size_t block_bytes = row_block_bytes(batch, heads, seq_len);
   const size_t kc_bytes = scaled_key_bytes(batch, heads, seq_len);
-  void* vt_space =
-      need > 0 ? static_cast<unsigned char*>(workspace) + 2 * norm_bytes + kc_bytes : nullptr;
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  void* vt_space = need > 0 ? base + norm_bytes + block_bytes + kc_bytes : nullptr;
+  const int64_t seq_pad = padded_seq(seq_len);
   int status = SAH_OK;
   prm.knorm = nullptr;
-  prm.qnorm = nullptr;
+  prm.kblock = nullptr;
+  prm.qblock = nullptr;
   prm.kc = nullptr;
   prm.key_tiles = (int)ceil_div(seq_len, 64);
-  // The pipelined kernel (num_stages 3) keeps the exact running maximum and
-  // never reads the table; its regions of the workspace then stay unused.
-  if (norm_bytes > 0 && num_stages != 3) {
-    unsigned char* base = static_cast<unsigned char*>(workspace);
-    float* norms = reinterpret_cast<float*>(base);
-    float* qnorms = reinterpret_cast<float*>(base + norm_bytes);
-    f16* kc = reinterpret_cast<f16*>(base + 2 * norm_bytes);
-    const bool zero_q = prm.q_and == 0u;
-    if (dtype == SAH_DTYPE_BF16) {
-      status = launch_key_norm<bf16>(key, norms, kc, prm.c, false, batch, heads, seq_len,
-                                     k_stride_b, k_stride_h, k_stride_s, stream);
-      if (status == SAH_OK)
-        status = launch_key_norm<bf16>(query, qnorms, nullptr, prm.c, zero_q, batch, heads,
-                                       seq_len, q_stride_b, q_stride_h, q_stride_s, stream);
-    } else {
-      status = launch_key_norm<f16>(key, norms, kc, prm.c, false, batch, heads, seq_len,
-                                    k_stride_b, k_stride_h, k_stride_s, stream);
-      if (status == SAH_OK)
-        status = launch_key_norm<f16>(query, qnorms, nullptr, prm.c, zero_q, batch, heads,
-                                      seq_len, q_stride_b, q_stride_h, q_stride_s, stream);
-    }
-    if (status != SAH_OK) return status;
-    prm.knorm = norms;
-    prm.qnorm = qnorms;
-    prm.kc = kc;
-  }
+  prm.num_row_blocks = (int)ceil_div(seq_len, kScaledKeyRows);
   if (v_stride_d == 1) {
-    // Reference layout: transpose V into the workspace first.
     if (!aligned16(value) || v_stride_b % 8 || v_stride_h % 8 || v_stride_s % 8)
       return fail(SAH_ERR_INVALID_ARGUMENT,
                   "value must be 16-byte aligned with strides multiple of 8");
-    status = (dtype == SAH_DTYPE_BF16)
-                 ? launch_transpose<bf16>(value, vt_space, batch, heads, seq_len,
-                                          v_stride_b, v_stride_h, v_stride_s, stream)
-                 : launch_transpose<f16>(value, vt_space, batch, heads, seq_len,
-                                         v_stride_b, v_stride_h, v_stride_s, stream);
-    if (status != SAH_OK) return status;
-    const int64_t seq_pad = padded_seq(seq_len);
-    prm.vt = vt_space;
-    prm.v_sb = heads * kHeadDim * seq_pad;
-    prm.v_sh = kHeadDim * seq_pad;
-    prm.v_sd = seq_pad;
   } else if (v_stride_s == 1) {
     if (!aligned16(value) || v_stride_b % 8 || v_stride_h % 8 || v_stride_d % 8)
       return fail(SAH_ERR_INVALID_ARGUMENT,
                   "seq-contiguous value must be 16-byte aligned with strides multiple of 8");
+  } else {
+    return fail(SAH_ERR_INVALID_ARGUMENT,
+                "value needs a unit stride on the head_dim or the seq axis");
+  }
+  // Long sequences (the plain kernel): one preparation launch writes the
+  // norm tables, the fp16 scaled keys and, for a head_dim-contiguous V, V^T.
+  // The pipelined kernel (num_stages 3) keeps the exact running maximum and
+  // never reads the tables; their regions of the workspace then stay unused.
+  const bool prepared = norm_bytes > 0 && num_stages != 3;
+  if (prepared) {
+    PrepParams pp;
+    pp.k = key;
+    pp.q = query;
+    pp.v = value;
+    pp.knorm = reinterpret_cast<float*>(base);
+    pp.kblock = reinterpret_cast<float*>(base + norm_bytes);
+    pp.qblock = pp.kblock + batch * heads * prm.num_row_blocks;
+    pp.kc = reinterpret_cast<f16*>(base + norm_bytes + block_bytes);
+    pp.vt = v_stride_d == 1 ? vt_space : nullptr;
+    pp.k_sb = k_stride_b;
+    pp.k_sh = k_stride_h;
+    pp.k_ss = k_stride_s;
+    pp.q_sb = q_stride_b;
+    pp.q_sh = q_stride_h;
+    pp.q_ss = q_stride_s;
+    pp.v_sb = v_stride_b;
+    pp.v_sh = v_stride_h;
+    pp.v_ss = v_stride_s;
+    pp.seq_pad = seq_pad;
+    pp.c = prm.c;
+    pp.zero_q = prm.q_and == 0u ? 1 : 0;
+    pp.heads = (int)heads;
+    pp.seq_len = (int)seq_len;
+    pp.key_tiles = prm.key_tiles;
+    pp.num_row_blocks = prm.num_row_blocks;
+    status = (dtype == SAH_DTYPE_BF16) ? launch_long_prepare<bf16>(pp, batch * heads, stream)
+                                       : launch_long_prepare<f16>(pp, batch * heads, stream);
+    if (status != SAH_OK) return status;
+    prm.knorm = pp.knorm;
+    prm.kblock = pp.kblock;
+    prm.qblock = pp.qblock;
+    prm.kc = pp.kc;
+  }
+  if (v_stride_d == 1) {
+    // Reference layout: V^T in the workspace (written by the preparation
+    // launch, or transposed here).
+    if (!prepared) {
+      status = (dtype == SAH_DTYPE_BF16)
+                   ? launch_transpose<bf16>(value, vt_space, batch, heads, seq_len,
+                                            v_stride_b, v_stride_h, v_stride_s, stream)
+                   : launch_transpose<f16>(value, vt_space, batch, heads, seq_len,
+                                           v_stride_b, v_stride_h, v_stride_s, stream);
+      if (status != SAH_OK) return status;
+    }
+    prm.vt = vt_space;
+    prm.v_sb = heads * kHeadDim * seq_pad;
+    prm.v_sh = kHeadDim * seq_pad;
+    prm.v_sd = seq_pad;
+  } else {
     prm.vt = value;
     prm.v_sb = v_stride_b;
     prm.v_sh = v_stride_h;
     prm.v_sd = v_stride_d;
-  } else {
-    return fail(SAH_ERR_INVALID_ARGUMENT,
-                "value needs a unit stride on the head_dim or the seq axis");
   }
   return (dtype == SAH_DTYPE_BF16)
              ? launch_attention<bf16>(prm, block_m, num_warps, num_stages, stream)

@@ -337,14 +337,22 @@ def test_scaled_key_path_sampled_rows(gpu_device, dtype, magnitude):
 
 
 def test_scaled_keys_in_the_workspace(gpu_device):
-    """The pre-pass writes the largest |k| and the largest |q| of every 64-row
-    tile into two tables, then every key times c = scale * log2(e) rounded to
-    fp16 as [batch*heads][key_tiles * 64][64]."""
+    """The preparation launch writes the largest |k| of every 64-key tile,
+    then the largest |k| and the largest |q| of every 512-row block, then
+    every key times c = scale * log2(e) rounded to fp16 as [batch*heads]
+    [key_tiles * 64][64].  Norms are checked against float64 norms of the
+    same rows (fp32 sums of squares: within a few ulps), the blocks against
+    the tiles' own maxima (bitwise: the same fp32 values, maximized), the
+    scaled keys bitwise against fp32 products rounded to fp16."""
 
     from solution.kernels.hip._library import load_library
 
     batch, heads, seq = 1, 3, 16_500
     q, k, v = _inputs(batch, heads, seq, dtype=torch.bfloat16, seed=12)
+    # one row of each of Q and K in the last block far above the rest, so a
+    # block maximum taken over the wrong rows shows
+    k[0, 1, 16_400] *= 5
+    q[0, 2, 16_499] *= 7
     library = load_library()
     vt = torch.zeros(batch, heads, 64, -(-seq // 64) * 64, dtype=torch.bfloat16)
     vt[..., :seq] = v.transpose(-2, -1)
@@ -352,8 +360,10 @@ def test_scaled_keys_in_the_workspace(gpu_device):
     value = vtd[..., :seq].transpose(-2, -1)
     need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 1, value.stride(3), 2)
     tiles = -(-seq // 64)
+    row_blocks = -(-seq // 512)
     table = -(-(batch * heads * tiles * 4) // 256) * 256
-    assert need == 2 * table + batch * heads * tiles * 64 * 64 * 2
+    block_bytes = -(-(2 * batch * heads * row_blocks * 4) // 256) * 256
+    assert need == table + block_bytes + batch * heads * tiles * 64 * 64 * 2
     workspace = torch.zeros(need, dtype=torch.uint8, device=gpu_device)
     out = torch.empty(batch, seq, heads * 64, dtype=torch.bfloat16, device=gpu_device)
     scale = 0.125
@@ -365,16 +375,27 @@ def test_scaled_keys_in_the_workspace(gpu_device):
     assert status == 0
     torch.cuda.synchronize()
     host = workspace.cpu()
+
+    def row_norms(x):
+        padded = torch.zeros(batch * heads, row_blocks * 512, 64, dtype=torch.float64)
+        padded[:, :seq] = x.double().reshape(batch * heads, seq, 64)
+        return padded.norm(dim=-1)
+
+    knorm64, qnorm64 = row_norms(k), row_norms(q)
     norms = host[: batch * heads * tiles * 4].view(torch.float32).view(batch * heads, tiles)
-    padded = torch.zeros(batch * heads, tiles * 64, 64)
-    padded[:, :seq] = k.float().reshape(batch * heads, seq, 64)
-    want_norms = padded.norm(dim=-1).view(batch * heads, tiles, 64).amax(-1)
-    assert torch.allclose(norms, want_norms, rtol=1e-5, atol=0)
-    qnorms = host[table : table + batch * heads * tiles * 4].view(torch.float32).view(batch * heads, tiles)
-    padded[:, :seq] = q.float().reshape(batch * heads, seq, 64)
-    want_qnorms = padded.norm(dim=-1).view(batch * heads, tiles, 64).amax(-1)
-    assert torch.allclose(qnorms, want_qnorms, rtol=1e-5, atol=0)
-    scaled = host[2 * table :].view(torch.float16).view(batch * heads, tiles * 64, 64)[:, :seq]
+    want_norms = knorm64[:, : tiles * 64].view(batch * heads, tiles, 64).amax(-1)
+    assert torch.allclose(norms.double(), want_norms, rtol=1e-5, atol=0)
+    start = table
+    kblock = host[start : start + batch * heads * row_blocks * 4].view(torch.float32).view(batch * heads, row_blocks)
+    start += batch * heads * row_blocks * 4
+    qblock = host[start : start + batch * heads * row_blocks * 4].view(torch.float32).view(batch * heads, row_blocks)
+    per_block = norms.new_zeros(batch * heads, row_blocks * 8)
+    per_block[:, :tiles] = norms
+    assert torch.equal(kblock, per_block.view(batch * heads, row_blocks, 8).amax(-1))
+    assert torch.allclose(kblock.double(), knorm64.view(batch * heads, row_blocks, 512).amax(-1), rtol=1e-5, atol=0)
+    assert torch.allclose(qblock.double(), qnorm64.view(batch * heads, row_blocks, 512).amax(-1), rtol=1e-5, atol=0)
+    assert int(kblock[1].argmax()) == row_blocks - 1 and int(qblock[2].argmax()) == row_blocks - 1
+    scaled = host[table + block_bytes :].view(torch.float16).view(batch * heads, tiles * 64, 64)[:, :seq]
     want = (k.float().reshape(batch * heads, seq, 64) * np.float32(scale * math.log2(math.e))).half()
     assert torch.equal(scaled, want)
 

@@ -57,19 +57,24 @@ def test_host_only_entry_points():
                     assert launch_config_is_valid(block_m, block_n, warps, stages) == bool(
                         library.sah_causal_attention_launch_supported(block_m, block_n, warps, stages)
                     ), (block_m, block_n, warps, stages)
-    # Sequences of 16384 keys or more get tables of the largest key norm and
-    # the largest query norm of every 64-row tile (fp32, each rounded up to
-    # 256 bytes) ...
+    # Sequences of 16384 keys or more get a table of the largest key norm of
+    # every 64-key tile (fp32, rounded up to 256 bytes) ...
     norms = -(-(2 * 16 * -(-100000 // 64) * 4) // 256) * 256
     assert norms == 200192
+    # ... two tables of the largest |k| and |q| of every 512-row block
+    # (fp32, together rounded up to 256 bytes) ...
+    blocks = -(-(2 * 2 * 16 * -(-100000 // 512) * 4) // 256) * 256
+    assert blocks == 50176
     # ... and every key times c in fp16, padded to 64 keys ...
     scaled_keys = 2 * 16 * 100032 * 64 * 2
     # ... followed, when V is head_dim-contiguous, by V^T padded to 64 keys.
     assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 3072, 1, 2) == (
-        2 * norms + scaled_keys + 2 * 16 * 64 * 100032 * 2
+        norms + blocks + scaled_keys + 2 * 16 * 64 * 100032 * 2
     )
-    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 1, 100032, 2) == 2 * norms + scaled_keys
-    assert library.sah_causal_attention_workspace_bytes(1, 16, 16384, 64, 1, 16384, 1) == 2 * 16 * 256 * 4 + 16 * 16384 * 128
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 1, 100032, 2) == norms + blocks + scaled_keys
+    assert library.sah_causal_attention_workspace_bytes(1, 16, 16384, 64, 1, 16384, 1) == (
+        16 * 256 * 4 + 2 * 16 * 32 * 4 + 16 * 16384 * 128
+    )
     # Shorter sequences need only the V^T buffer, and seq-contiguous V none.
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 64, 1, 2) == 8 * 16 * 64 * 2048 * 2
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 1, 2048, 2) == 0
