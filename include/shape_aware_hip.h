@@ -66,15 +66,19 @@ const char* sah_last_error(void);
  *
  * dtype: SAH_DTYPE_BF16 or SAH_DTYPE_F16 for q, k, v and output.
  * q/k: the head_dim stride must be 1, the seq stride a multiple of 8 and the
- *      base 16-byte aligned.
+ *      base 16-byte aligned; the key seq stride must lie in [0, 2^24).
  * v:   either head_dim-contiguous (v_stride_d == 1, the reference layout; the
- *      kernel then first writes V^T into `workspace`) or seq-contiguous
- *      (v_stride_s == 1, a V^T buffer).
+ *      kernel then first writes V^T into `workspace`, so seq_len rounded up
+ *      to 64 must stay below 2^24) or seq-contiguous (v_stride_s == 1, a V^T
+ *      buffer whose v_stride_d must lie in [0, 2^24)).  Tiles of 64 key rows
+ *      are addressed at 32-bit offsets; larger strides return
+ *      SAH_ERR_UNSUPPORTED.
  * workspace: 16-byte aligned, at least sah_causal_attention_workspace_bytes();
  *      may be null when that is 0.  Sequences of 16384 keys or more keep
- *      there, written by a pre-pass over K and Q: tables of the largest key
- *      norm and query norm of every 64-row tile, which bound every score so
- *      that most tiles skip their row maximum, and the keys times
+ *      there, written by one preparation launch over Q, K (and V): a table
+ *      of the largest key norm of every 64-key tile, which bounds every score
+ *      so that most tiles skip their row maximum, tables of the largest key
+ *      and query norm of every 512-row block, and the keys times
  *      scale * log2(e) in fp16.  A block of 512 query rows whose bound
  *      scale * log2(e) * max|q| * max|k| is at most 32 (15 for fp16) computes
  *      its scores on the fp16 MFMA from those keys and takes P = exp2(score)

@@ -206,6 +206,15 @@ __device__ __forceinline__ u32x4 load8_guarded(const T* src, int64_t first,
   return __builtin_bit_cast(u32x4, v);
 }
 
+// Buffer resource over the bytes from `base` on (raw, unchecked range), and
+// a 16-byte load at a 32-bit byte offset from it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
 // Cross-half reductions: lanes l and l^32 hold the two key halves of one
 // query row.  v_permlane32_swap exchanges the halves of two registers; the max
 // (or sum) of the two results is the cross-half value in every lane, whichever
@@ -251,7 +260,10 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave index in a scalar register on the scaled-key path, so its per-tile
+  // wave conditions are scalar compares; the other paths keep it in a VGPR
+  // (a scalar copy there raised their register use with no measured gain).
+  const int wave = (PATH == kPathScaled) ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
@@ -333,31 +345,53 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   const int64_t kss = SCALED ? (int64_t)kHeadDim : p.k_ss;
 
   // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
+  // Full tiles are read as buffer loads: a tile base in scalar registers
+  // plus this thread's 32-bit byte offset inside the tile (the host keeps
+  // 64 rows of K and of V^T within 2^31 bytes).
+  uint32_t k_off[CPT], v_off[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int chunk = tid + NT * i;
+    const int row = chunk >> 3;
+    const int c8 = (chunk & 7) * 8;
+    k_off[i] = (uint32_t)(((int64_t)row * kss + c8) * (int64_t)sizeof(T));
+    v_off[i] = (uint32_t)(((int64_t)row * p.v_sd + c8) * (int64_t)sizeof(T));
+  }
   u32x4 k_pref[CPT], v_pref[CPT];
   auto load_tile = [&](int tile) {
     const int k0 = tile * kBlockN;
     if (k0 + kBlockN <= S) {  // tile-uniform: every key of the tile exists
+      const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + (int64_t)k0 * kss);
+      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + k0);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int chunk = tid + NT * i;
-        const int row = chunk >> 3;
-        const int c8 = (chunk & 7) * 8;
-        k_pref[i] = load16(kb + (int64_t)(k0 + row) * kss + c8);
-        v_pref[i] = load16(vbase + (int64_t)row * p.v_sd + k0 + c8);
+        k_pref[i] = buffer_load16(kr, k_off[i]);
+        v_pref[i] = buffer_load16(vr, v_off[i]);
       }
     } else {
+      const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + (int64_t)k0 * kss);
+      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + k0);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         const int chunk = tid + NT * i;
         const int row = chunk >> 3;
         const int c8 = (chunk & 7) * 8;
-        const int key = k0 + row;
         u32x4 raw = {0u, 0u, 0u, 0u};
-        if (key < S) raw = load16(kb + (int64_t)key * kss + c8);
+        if (k0 + row < S) raw = buffer_load16(kr, k_off[i]);
         k_pref[i] = raw;
-        // V^T: row = head-dim index, 8 consecutive keys.
-        v_pref[i] = load8_guarded<T>(vbase + (int64_t)row * p.v_sd + k0 + c8,
-                                     (int64_t)k0 + c8, S);
+        // V^T: row = head-dim index, 8 consecutive keys from k0 + c8.
+        const int valid = S - k0 - c8;
+        if (valid >= 8) {
+          v_pref[i] = buffer_load16(vr, v_off[i]);
+        } else {
+          uint32_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            h[e] = (e < valid) ? (uint32_t)__builtin_bit_cast(
+                                     unsigned short, __builtin_amdgcn_raw_buffer_load_b16(vr, v_off[i] + 2 * e, 0, 0))
+                               : 0u;
+          v_pref[i] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        }
       }
     }
   };
@@ -413,143 +447,154 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   __syncthreads();
   float kn_next = bounded ? knorm[0] : 0.0f;
 
-  for (int j = 0; j < n_tiles; ++j) {
-    const int stage = (STAGES == 2) ? (j & 1) : 0;
-    const bool has_next = j + 1 < n_tiles;
-    if (has_next) load_tile(j + 1);
-    const float kn = kn_next;
-    if (bounded && has_next) kn_next = knorm[j + 1];
-    const int k0 = j * kBlockN;
+  // Tile loop.  On the scaled-key path with two LDS stages it runs two
+  // tiles per iteration (the inner loop is unrolled), so each copy's stage
+  // is a constant and the LDS operand reads and stores use immediate
+  // offsets; the other paths keep one tile per iteration (two copies of
+  // their larger state spill).
+  constexpr int kStep = (STAGES == 2 && PATH == kPathScaled) ? 2 : 1;
+  for (int j0 = 0; j0 < n_tiles; j0 += kStep) {
+#pragma unroll
+    for (int u = 0; u < kStep; ++u) {
+      const int j = j0 + u;
+      if (kStep > 1 && j >= n_tiles) break;
+      const int stage = (kStep > 1) ? u : ((STAGES == 2) ? (j & 1) : 0);
+      const bool has_next = j + 1 < n_tiles;
+      if (has_next) load_tile(j + 1);
+      const float kn = kn_next;
+      if (bounded && has_next) kn_next = knorm[j + 1];
+      const int k0 = j * kBlockN;
 
-    if (k0 <= wq_last) {  // wave-uniform: skip tiles entirely above this wave's rows
-      // S^T[key][query] for 2 subtiles of 32 keys; on the scaled-key path
-      // both operands hold fp16 bits and the result is c q.k.
-      f32x16 sacc[QG][2];
+      if (k0 <= wq_last) {  // wave-uniform: skip tiles entirely above this wave's rows
+        // S^T[key][query] for 2 subtiles of 32 keys; on the scaled-key path
+        // both operands hold fp16 bits and the result is c q.k.
+        f32x16 sacc[QG][2];
 #pragma unroll
-      for (int g = 0; g < QG; ++g)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[g][t][r] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const V8 a = *reinterpret_cast<const V8*>(
-              &k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
-#pragma unroll
-          for (int g = 0; g < QG; ++g)
-            if constexpr (SCALED)
-              sacc[g][t] = mfma32(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, qop[g][s]),
-                                  sacc[g][t]);
-            else
-              sacc[g][t] = mfma32(a, qop[g][s], sacc[g][t]);
-        }
-      }
-
-      // Causal mask: only tiles that reach past this wave's first query.
-      // Element r of subtile t is key k0 + 32 t + 16 (r / 8) + 8 half + r % 8;
-      // it is masked when that exceeds the lane's query, i.e. when the
-      // constant 32 t + 16 (r / 8) + r % 8 exceeds qi - k0 - 8 half (one
-      // compare against an immediate per element).
-      if (k0 + kBlockN - 1 > wq0) {
-#pragma unroll
-        for (int g = 0; g < QG; ++g) {
-          const int lim = wq0 + 32 * g + l32 - k0 - 8 * half;
+        for (int g = 0; g < QG; ++g)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (32 * t + 16 * (r >> 3) + (r & 7) > lim) sacc[g][t][r] = -INFINITY;
-        }
-      }
-
-      V8 pb[QG][4];
+            for (int r = 0; r < 16; ++r) sacc[g][t][r] = 0.0f;
 #pragma unroll
-      for (int g = 0; g < QG; ++g) {
-        float lsum = l_run[g];
-        if constexpr (SCALED) {
-          // P = exp2(c q.k): every score lies within the bound, no shift.
+        for (int s = 0; s < 4; ++s) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int t = u >> 1;
-            const int rb = (u & 1) * 8;
-            V8 pk;
+          for (int t = 0; t < 2; ++t) {
+            const V8 a = *reinterpret_cast<const V8*>(
+                &k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-              V2 pair;
-              pair[0] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e]);
-              pair[1] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e + 1]);
-              lsum = dot2_sum(pair, lsum);
-              pk[e] = pair[0];
-              pk[e + 1] = pair[1];
-            }
-            pb[g][u] = pk;
+            for (int g = 0; g < QG; ++g)
+              if constexpr (SCALED)
+                sacc[g][t] = mfma32(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, qop[g][s]),
+                                    sacc[g][t]);
+              else
+                sacc[g][t] = mfma32(a, qop[g][s], sacc[g][t]);
           }
-        } else {
-          // Rows whose bound keeps every probability below 2^safe_exponent skip the
-          // tile maximum.  Rows that need it move their shift up to the tile
-          // maximum only when that exceeds it by more than kLazyShift (log2
-          // units), so the O rescale is rare.  Both decisions are per row, so
-          // results do not depend on the launch.
-          const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
-          if (__any(need)) {
-            float mx = sacc[g][0][0];
+        }
+
+        // Causal mask: only tiles that reach past this wave's first query.
+        // Element r of subtile t is key k0 + 32 t + 16 (r / 8) + 8 half + r % 8;
+        // it is masked when that exceeds the lane's query, i.e. when the
+        // constant 32 t + 16 (r / 8) + r % 8 exceeds qi - k0 - 8 half (one
+        // compare against an immediate per element).
+        if (k0 + kBlockN - 1 > wq0) {
+#pragma unroll
+          for (int g = 0; g < QG; ++g) {
+            const int lim = wq0 + 32 * g + l32 - k0 - 8 * half;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-              for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
-            mx = half_swap_max(mx);
-            const bool grow = need && (mx - m_run[g]) * c > kLazyShift;
-            if (__any(grow)) {
-              const float m_new = grow ? mx : m_run[g];
-              const float alpha = exp2f((m_run[g] - m_new) * c);
-              lsum *= alpha;
-#pragma unroll
-              for (int d = 0; d < 2; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
-              m_run[g] = m_new;
-            }
-          }
-          const float mc = m_run[g] * c;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int t = u >> 1;
-            const int rb = (u & 1) * 8;
-            V8 pk;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-              V2 pair;
-              pair[0] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e], c, -mc));
-              pair[1] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e + 1], c, -mc));
-              lsum = dot2_sum(pair, lsum);
-              pk[e] = pair[0];
-              pk[e + 1] = pair[1];
-            }
-            pb[g][u] = pk;
+              for (int r = 0; r < 16; ++r)
+                if (32 * t + 16 * (r >> 3) + (r & 7) > lim) sacc[g][t][r] = -INFINITY;
           }
         }
-        l_run[g] = lsum;
-      }
 
-      // O^T[dh][query] += V^T[dh][keys] P^T[keys][query]
+        V8 pb[QG][4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+        for (int g = 0; g < QG; ++g) {
+          float lsum = l_run[g];
+          if constexpr (SCALED) {
+            // P = exp2(c q.k): every score lies within the bound, no shift.
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const V8 a = *reinterpret_cast<const V8*>(
-              &v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+            for (int u = 0; u < 4; ++u) {
+              const int t = u >> 1;
+              const int rb = (u & 1) * 8;
+              V8 pk;
 #pragma unroll
-          for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(a, pb[g][u], acc[g][d]);
+              for (int e = 0; e < 8; e += 2) {
+                V2 pair;
+                pair[0] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e]);
+                pair[1] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e + 1]);
+                lsum = dot2_sum(pair, lsum);
+                pk[e] = pair[0];
+                pk[e + 1] = pair[1];
+              }
+              pb[g][u] = pk;
+            }
+          } else {
+            // Rows whose bound keeps every probability below 2^safe_exponent skip the
+            // tile maximum.  Rows that need it move their shift up to the tile
+            // maximum only when that exceeds it by more than kLazyShift (log2
+            // units), so the O rescale is rare.  Both decisions are per row, so
+            // results do not depend on the launch.
+            const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
+            if (__any(need)) {
+              float mx = sacc[g][0][0];
+#pragma unroll
+              for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[g][t][r]);
+              mx = half_swap_max(mx);
+              const bool grow = need && (mx - m_run[g]) * c > kLazyShift;
+              if (__any(grow)) {
+                const float m_new = grow ? mx : m_run[g];
+                const float alpha = exp2f((m_run[g] - m_new) * c);
+                lsum *= alpha;
+#pragma unroll
+                for (int d = 0; d < 2; ++d)
+#pragma unroll
+                  for (int r = 0; r < 16; ++r) acc[g][d][r] *= alpha;
+                m_run[g] = m_new;
+              }
+            }
+            const float mc = m_run[g] * c;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int t = u >> 1;
+              const int rb = (u & 1) * 8;
+              V8 pk;
+#pragma unroll
+              for (int e = 0; e < 8; e += 2) {
+                V2 pair;
+                pair[0] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e], c, -mc));
+                pair[1] = (T)__builtin_amdgcn_exp2f(fmaf(sacc[g][t][rb + e + 1], c, -mc));
+                lsum = dot2_sum(pair, lsum);
+                pk[e] = pair[0];
+                pk[e + 1] = pair[1];
+              }
+              pb[g][u] = pk;
+            }
+          }
+          l_run[g] = lsum;
+        }
+
+        // O^T[dh][query] += V^T[dh][keys] P^T[keys][query]
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const V8 a = *reinterpret_cast<const V8*>(
+                &v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+#pragma unroll
+            for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(a, pb[g][u], acc[g][d]);
+          }
         }
       }
-    }
 
-    if (has_next) {
-      if (STAGES == 1) __syncthreads();  // everyone done reading the single buffer
-      store_tile(STAGES == 2 ? ((j + 1) & 1) : 0);
-      __syncthreads();
+      if (has_next) {
+        if (STAGES == 1) __syncthreads();  // everyone done reading the single buffer
+        store_tile(STAGES == 2 ? ((j + 1) & 1) : 0);
+        __syncthreads();
+      }
     }
   }
 
@@ -1559,6 +1604,14 @@ extern "C" int sah_causal_attention_bsd(
     return fail(SAH_ERR_INVALID_ARGUMENT,
                 "value needs a unit stride on the head_dim or the seq axis");
   }
+  // The tile loaders address 64 rows of K and of V^T at 32-bit byte offsets
+  // from a per-tile base: both row strides must be non-negative and 64 rows
+  // must span less than 2^31 bytes.
+  const int64_t vt_row_stride = (v_stride_d == 1) ? seq_pad : v_stride_d;
+  if (k_stride_s < 0 || vt_row_stride < 0 || k_stride_s >= ((int64_t)1 << 24) ||
+      vt_row_stride >= ((int64_t)1 << 24))
+    return fail(SAH_ERR_UNSUPPORTED,
+                "key/value row strides must lie in [0, 2^24) elements (32-bit tile offsets)");
   // Long sequences (the plain kernel): one preparation launch writes the
   // norm tables, the fp16 scaled keys and, for a head_dim-contiguous V, V^T.
   // The pipelined kernel (num_stages 3) keeps the exact running maximum and

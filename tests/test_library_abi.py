@@ -94,6 +94,21 @@ def test_invalid_arguments_fail_before_launch():
         fake, fake, fake, fake, 1, 1, 16, 32, *([0] * 12), 0.125, 2, 128, 64, 4, 2, None, 0, None
     )
     assert status == _library.SAH_ERR_UNSUPPORTED and b"head_dim" in library.sah_last_error()
+    # Tiles of 64 key rows are addressed at 32-bit offsets: key and V^T row
+    # strides outside [0, 2^24) elements are refused before any launch.
+    def attend(seq, k_ss, v_ss, v_sd, workspace=None, workspace_bytes=0):
+        return library.sah_causal_attention_bsd(
+            fake, fake, fake, fake, 1, 1, seq, 64, 0, 0, 64, 0, 0, k_ss, 0, 0, v_ss, v_sd, 0, 64,
+            0.125, 2, 128, 64, 4, 2, workspace, workspace_bytes, None)
+
+    for k_ss, v_sd in ((-64, 1024), (1 << 24, 1024), (64, 1 << 24), (64, -1024)):
+        assert attend(1000, k_ss, 1, v_sd) == _library.SAH_ERR_UNSUPPORTED, (k_ss, v_sd)
+        assert b"32-bit tile offsets" in library.sah_last_error()
+    # the reference V layout stages V^T with rows of roundup(seq, 64) keys
+    long_seq = (1 << 24) + 1
+    need = library.sah_causal_attention_workspace_bytes(1, 1, long_seq, 64, 64, 1, 2)
+    assert attend(long_seq, 64, 64, 1, fake, need) == _library.SAH_ERR_UNSUPPORTED
+    assert b"32-bit tile offsets" in library.sah_last_error()
     status = library.sah_residual_norm(
         fake, fake, None, None, fake, fake, 4, 1000, 1e-5, 2, 2, 2, 0, 0, 4, 4, None
     )
