@@ -178,6 +178,12 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ float dot2_sum(bf16x2 p, float acc) {
   const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
@@ -213,6 +219,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
 }
 __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t offset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+
+// Direct-to-LDS tile ring (scaled-key path): tile rows of 128 bytes, chunk c
+// (8 elements) of row r in 16-byte slot c ^ ring_swizzle(r).  The swizzle
+// keeps the operand reads of every 8- and 16-lane group on distinct slots
+// (rows 0..15 in the order the score and PV reads visit them).
+__device__ __forceinline__ int ring_swizzle(int r) {
+  return ((r >> 1) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
+}
+// One 16-byte direct-to-LDS load per lane: lane i's bytes from
+// base + offset land at LDS byte lds + 16 i (base and lds wave-uniform,
+// moved to scalar registers here).  Written as assembly so the compiler does
+// not treat it as an LDS write (it would wait for it before every LDS read);
+// the tile loop waits for it explicitly.
+__device__ __forceinline__ void dma16(const void* base, uint32_t offset, uint32_t lds) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint64_t sbase = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(offset), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
+// s_waitcnt with at most n vector-memory operations outstanding (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt left open).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 // Cross-half reductions: lanes l and l^32 hold the two key halves of one
@@ -255,8 +289,16 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   constexpr int NT = WAVES * 64;             // threads
   constexpr int CPT = (kBlockN * 8) / NT;    // 16-byte chunks of a tile per thread
 
-  __shared__ __attribute__((aligned(16))) T k_lds[STAGES][kBlockN][kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[STAGES][kHeadDim][kVRow];
+  // The scaled-key path of the 8-wave, 32-rows-per-wave launch stages K and
+  // V^T by direct-to-LDS loads into a ring of three tiles (two in flight
+  // while one is read); the other kernels use padded double buffers filled
+  // through registers.
+  constexpr bool kDma = PATH == kPathScaled && STAGES == 2 && WAVES == 8 && QG == 1;
+  constexpr int kRing = 3;
+  constexpr int kRingStage = 2 * kBlockN * kHeadDim * (int)sizeof(T);  // K then V^T, 16 KiB
+  __shared__ __attribute__((aligned(16))) T k_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kKRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[kDma ? 1 : STAGES][kDma ? 1 : kHeadDim][kDma ? 8 : kVRow];
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[kDma ? kRing * kRingStage : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -344,6 +386,8 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
                        : kbase;
   const int64_t kss = SCALED ? (int64_t)kHeadDim : p.k_ss;
 
+  const int a_row = k_row_for(l32);
+
   // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
   // Full tiles are read as buffer loads: a tile base in scalar registers
   // plus this thread's 32-bit byte offset inside the tile (the host keeps
@@ -406,9 +450,93 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     }
   };
 
+  // Ring loader (kDma): the 16 bytes of lane l of wave w land at tile row
+  // dr = 8 w + l / 8, slot l % 8, so they carry logical chunk
+  // dc = (l % 8) ^ ring_swizzle(dr) of that row of K and of V^T.
+  const int dr = wave * 8 + (lane >> 3);
+  const int dc = (lane & 7) ^ ring_swizzle(dr);
+  const uint32_t k_ring_off = (uint32_t)(((int64_t)dr * kss + 8 * dc) * (int64_t)sizeof(T));
+  const uint32_t v_ring_off = (uint32_t)(((int64_t)dr * p.v_sd + 8 * dc) * (int64_t)sizeof(T));
+  const uint32_t ring_lds =
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) unsigned char*)ring);
+  // Fills ring stage `stage` with tile `tile`; returns whether it issued
+  // direct-to-LDS loads (two per lane).  A tile that reaches past the
+  // sequence goes through registers, zero-filled, into the same slots.
+  auto fill_ring = [&](int tile, int stage) -> bool {
+    const int k0 = tile * kBlockN;
+    const T* kt = kb + (int64_t)k0 * kss;
+    const T* vt = vbase + k0;
+    const uint32_t dst = ring_lds + stage * kRingStage + wave * 1024;
+    if (k0 + kBlockN <= S) {
+      dma16(kt, k_ring_off, dst);
+      dma16(vt, v_ring_off, dst + kRingStage / 2);
+      return true;
+    }
+    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kt);
+    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vt);
+    u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
+    if (k0 + dr < S) kraw = buffer_load16(kr, k_ring_off);
+    const int valid = S - k0 - 8 * dc;
+    if (valid >= 8) {
+      vraw = buffer_load16(vr, v_ring_off);
+    } else {
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        h[e] = (e < valid) ? (uint32_t)__builtin_bit_cast(
+                                 unsigned short, __builtin_amdgcn_raw_buffer_load_b16(vr, v_ring_off + 2 * e, 0, 0))
+                           : 0u;
+      vraw = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    unsigned char* slot = ring + stage * kRingStage + wave * 1024 + lane * 16;
+    *reinterpret_cast<u32x4*>(slot) = kraw;
+    *reinterpret_cast<u32x4*>(slot + kRingStage / 2) = vraw;
+    return false;
+  };
+  // Operand fragments: K rows 32 t + a_row, chunk 2 s + half; V^T rows
+  // 32 d + l32, chunk 2 u + half.  In the ring, their byte offsets inside a
+  // stage are kept for the whole loop, so every operand read is one register
+  // plus an immediate (stage, subtile).
+  uint32_t k_ring_at[4], v_ring_at[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k_ring_at[i] = (uint32_t)(a_row * 128 + (((2 * i + half) ^ ring_swizzle(a_row)) << 4));
+    v_ring_at[i] = (uint32_t)(l32 * 128 + (((2 * i + half) ^ ring_swizzle(l32)) << 4));
+  }
+  auto k_frag = [&](int stage, int t, int s) -> V8 {
+    if constexpr (kDma)
+      return *reinterpret_cast<const V8*>(ring + stage * kRingStage + 32 * t * 128 + k_ring_at[s]);
+    else
+      return *reinterpret_cast<const V8*>(&k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
+  };
+  auto v_frag = [&](int stage, int d, int u) -> V8 {
+    if constexpr (kDma)
+      return *reinterpret_cast<const V8*>(ring + stage * kRingStage + kRingStage / 2 + 32 * d * 128 +
+                                          v_ring_at[u]);
+    else
+      return *reinterpret_cast<const V8*>(&v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+  };
+
   // ---- running state (lane-local: query l32 of each group).
   f32x16 acc[QG][2];
   float m_run[QG], l_run[QG];
+  // Scaled-key path: the row sums run on the matrix cores.  Read as the B
+  // operand of a 16x16x32 product, a P^T fragment holds, in lane 16 kg + n,
+  // the 8 probabilities of query n + 16 (kg % 2) for keys 8 (kg / 2) .. of
+  // its 16-key slice; A = `ones` (row 0 ones for kg even, row 1 for kg odd)
+  // makes C[0][n] and C[1][n] the slice sums of queries n and n + 16, which
+  // accumulate over the slices into lanes 0..15 of rsum.
+  f32x4 rsum[QG];
+  V8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (T)0.0f;
+  if constexpr (SCALED) {
+    const bool one_lane = (lane == 0 || lane == 32 || lane == 17 || lane == 49);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = one_lane ? (T)1.0f : (T)0.0f;
+  }
+#pragma unroll
+  for (int g = 0; g < QG; ++g) rsum[g] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
     m_run[g] = -INFINITY;
@@ -419,7 +547,6 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       for (int r = 0; r < 16; ++r) acc[g][d][r] = 0.0f;
   }
   const float c = p.c;
-  const int a_row = k_row_for(l32);
   const bool bounded = p.knorm != nullptr;  // uniform
   // Global address space spelled out: the table entry of the next tile is
   // then a scalar load (uniform address, read-only).  Left to inference the
@@ -442,17 +569,23 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       }
   }
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  bool ring_next = false;  // the next ring tile was issued as direct-to-LDS loads
+  if constexpr (kDma) {
+    fill_ring(0, 0);
+    ring_next = n_tiles > 1 && fill_ring(1, 1);
+  } else {
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+  }
   float kn_next = bounded ? knorm[0] : 0.0f;
 
-  // Tile loop.  On the scaled-key path with two LDS stages it runs two
-  // tiles per iteration (the inner loop is unrolled), so each copy's stage
-  // is a constant and the LDS operand reads and stores use immediate
-  // offsets; the other paths keep one tile per iteration (two copies of
-  // their larger state spill).
-  constexpr int kStep = (STAGES == 2 && PATH == kPathScaled) ? 2 : 1;
+  // Tile loop.  On the scaled-key path it runs two tiles per iteration with
+  // two LDS stages, or three with the ring (the inner loop is unrolled), so
+  // each copy's stage is a constant and the LDS operand reads and stores use
+  // immediate offsets; the other paths keep one tile per iteration (two
+  // copies of their larger state spill).
+  constexpr int kStep = kDma ? kRing : ((STAGES == 2 && PATH == kPathScaled) ? 2 : 1);
   for (int j0 = 0; j0 < n_tiles; j0 += kStep) {
 #pragma unroll
     for (int u = 0; u < kStep; ++u) {
@@ -460,7 +593,23 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       if (kStep > 1 && j >= n_tiles) break;
       const int stage = (kStep > 1) ? u : ((STAGES == 2) ? (j & 1) : 0);
       const bool has_next = j + 1 < n_tiles;
-      if (has_next) load_tile(j + 1);
+      if constexpr (kDma) {
+        // Tile j has landed once only the next tile's loads (if it was
+        // issued to the ring) remain; the barrier then also retires every
+        // wave's reads of the stage refilled below (tile j - 1's).
+        if (ring_next)
+          wait_vmcnt<2>();
+        else
+          wait_vmcnt<0>();
+        __builtin_amdgcn_s_waitcnt(0xc07f & ~(0xF << 8));  // lgkmcnt(0): register-path stores
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        // From here on ring_next describes tile j + 2, the next wait's.
+        ring_next = j + 2 < n_tiles && fill_ring(j + 2, (u + 2) % kRing);
+      } else {
+        if (has_next) load_tile(j + 1);
+      }
       const float kn = kn_next;
       if (bounded && has_next) kn_next = knorm[j + 1];
       const int k0 = j * kBlockN;
@@ -479,8 +628,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
-            const V8 a = *reinterpret_cast<const V8*>(
-                &k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
+            const V8 a = k_frag(stage, t, s);
 #pragma unroll
             for (int g = 0; g < QG; ++g)
               if constexpr (SCALED)
@@ -524,11 +672,11 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
                 V2 pair;
                 pair[0] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e]);
                 pair[1] = (T)__builtin_amdgcn_exp2f(sacc[g][t][rb + e + 1]);
-                lsum = dot2_sum(pair, lsum);
                 pk[e] = pair[0];
                 pk[e + 1] = pair[1];
               }
               pb[g][u] = pk;
+              rsum[g] = mfma16(ones, pk, rsum[g]);
             }
           } else {
             // Rows whose bound keeps every probability below 2^safe_exponent skip the
@@ -582,15 +730,14 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
         for (int u = 0; u < 4; ++u) {
 #pragma unroll
           for (int d = 0; d < 2; ++d) {
-            const V8 a = *reinterpret_cast<const V8*>(
-                &v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+            const V8 a = v_frag(stage, d, u);
 #pragma unroll
             for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(a, pb[g][u], acc[g][d]);
           }
         }
       }
 
-      if (has_next) {
+      if (!kDma && has_next) {
         if (STAGES == 1) __syncthreads();  // everyone done reading the single buffer
         store_tile(STAGES == 2 ? ((j + 1) & 1) : 0);
         __syncthreads();
@@ -602,7 +749,14 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 #pragma unroll
   for (int g = 0; g < QG; ++g) {
     const int qi = wq0 + 32 * g + l32;
-    const float l_tot = half_swap_sum(l_run[g]);
+    float l_tot;
+    if constexpr (SCALED) {
+      const float lo = __shfl(rsum[g][0], l32 & 15);
+      const float hi = __shfl(rsum[g][1], l32 & 15);
+      l_tot = l32 < 16 ? lo : hi;
+    } else {
+      l_tot = half_swap_sum(l_run[g]);
+    }
     if (qi >= S) continue;
     const float inv = 1.0f / l_tot;
     T* orow = obase + (int64_t)qi * p.o_ss;
