@@ -283,16 +283,20 @@ def gpu_benchmark(steps: int, warmup: int, *, check: bool = True) -> dict:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "attn_fwd_c5_chunk_traffic.md"
-ATTENTION_SOURCE = PACKAGE_DIR / "csrc" / "attention_fwd.hip"
+ATTENTION_SOURCES = tuple(
+    PACKAGE_DIR / "csrc" / name for name in ("attention_kernel.hpp", "attention_fwd.hip", "attention_scaled.hip")
+)
 
 
 def attention_source_digest() -> str:
     """Digest of what the traffic figure depends on: the attention kernel
-    source and the launch the long-sequence program uses."""
+    sources and the launch the long-sequence program uses."""
 
     from solution.config import HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
 
-    digest = hashlib.sha256(ATTENTION_SOURCE.read_bytes())
+    digest = hashlib.sha256()
+    for path in ATTENTION_SOURCES:
+        digest.update(path.read_bytes())
     digest.update(repr(HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).encode())
     return digest.hexdigest()[:16]
 
