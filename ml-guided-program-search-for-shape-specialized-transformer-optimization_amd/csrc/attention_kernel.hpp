@@ -259,11 +259,11 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   constexpr int NT = WAVES * 64;             // threads
   constexpr int CPT = (kBlockN * 8) / NT;    // 16-byte chunks of a tile per thread
 
-  // The scaled-key path of the 8-wave, 32-rows-per-wave launch stages K and
-  // V^T by direct-to-LDS loads into a ring of three tiles (two in flight
-  // while one is read); the other kernels use padded double buffers filled
-  // through registers.
-  constexpr bool kDma = PATH == kPathScaled && STAGES == 2 && WAVES == 8 && QG == 1;
+  // The scaled-key path of the 8-wave launches (32 or 64 rows per wave)
+  // stages K and V^T by direct-to-LDS loads into a ring of three tiles (two
+  // in flight while one is read); the other kernels use padded double
+  // buffers filled through registers.
+  constexpr bool kDma = PATH == kPathScaled && STAGES == 2 && WAVES == 8;
   constexpr int kRing = 3;
   constexpr int kRingStage = 2 * kBlockN * kHeadDim * (int)sizeof(T);  // K then V^T, 16 KiB
   __shared__ __attribute__((aligned(16))) T k_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kKRow];
