@@ -149,6 +149,36 @@ def test_packed_qkv_view_and_transposed_value_layouts_agree(gpu_device):
     _assert_parity(reference, from_view, torch.bfloat16, "packed view")
 
 
+@pytest.mark.parametrize("block_m,num_warps", [(256, 8), (512, 8), (128, 4)])
+def test_long_sequence_value_layouts_agree_with_poisoned_padding(gpu_device, block_m, num_warps):
+    """S = 16500 (scaled-key path; the last key tile is partial, and so is its
+    last 8-key chunk): V as the packed head_dim-contiguous view (staged into
+    the workspace's zero-padded V^T) and as a caller's seq-contiguous V^T
+    buffer whose columns past the sequence hold NaN give bitwise equal
+    outputs, so the staging never reads a key at or past S (a NaN times
+    P = 0 would show)."""
+
+    batch, seq, heads = 1, 16_500, 2
+    width = heads * 64
+    print(f"value layouts S={seq} launch=({block_m}, {num_warps}, 2)", flush=True)
+    generator = torch.Generator().manual_seed(29)
+    packed = torch.randn(batch, seq, 3 * width, generator=generator).to(torch.bfloat16).to(gpu_device)
+    q, k, v = (t.transpose(1, 2) for t in packed.unflatten(-1, (3, heads, 64)).unbind(dim=2))
+    module = _attention_module()
+    launch = dict(block_m=block_m, block_n=64, num_warps=num_warps, num_stages=2)
+    with torch.inference_mode():
+        from_view, _ = module.hip_streaming_dh64_causal_attention_bsd(q, k, v, scale=1 / 8, **launch)
+        stride = seq + 12  # a multiple of 8 that leaves a partial chunk of padding after S
+        v_t = torch.full((batch, heads, 64, stride), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+        v_t[..., :seq] = v.transpose(-1, -2)
+        v_seq_major = v_t[..., :seq].transpose(-1, -2)
+        assert v_seq_major.stride(-2) == 1 and v_seq_major.stride(-1) == stride
+        from_vt, _ = module.hip_streaming_dh64_causal_attention_bsd(q, k, v_seq_major, scale=1 / 8, **launch)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(from_view).all())
+    assert torch.equal(from_view, from_vt)
+
+
 def test_constant_value_rows_are_reproduced(gpu_device):
     """Softmax weights sum to one, so a constant V column yields that constant."""
 
