@@ -609,6 +609,11 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
           }
         }
 
+        // Scaled-key path: the wave's exponential phase runs at raised
+        // priority, so among the waves of a SIMD the one converting scores
+        // to P issues first and the next MFMAs find their operands sooner
+        // (priority during the MFMA phases instead measured 3.8% slower).
+        if constexpr (SCALED) __builtin_amdgcn_s_setprio(1);
         // Causal mask: only tiles that reach past this wave's first query.
         // Element r of subtile t is key k0 + 32 t + 16 (r / 8) + 8 half + r % 8;
         // it is masked when that exceeds the lane's query, i.e. when the
@@ -695,6 +700,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
           l_run[g] = lsum;
         }
 
+        if constexpr (SCALED) __builtin_amdgcn_s_setprio(0);
         // O^T[dh][query] += V^T[dh][keys] P^T[keys][query]
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
