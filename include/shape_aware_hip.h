@@ -74,7 +74,7 @@ const char* sah_last_error(void);
  *      are addressed at 32-bit offsets; larger strides return
  *      SAH_ERR_UNSUPPORTED.
  * workspace: 16-byte aligned, at least sah_causal_attention_workspace_bytes();
- *      may be null when that is 0.  Sequences of 16384 keys or more keep
+ *      may be null when that is 0.  Sequences of 4096 keys or more keep
  *      there, written by one preparation launch over Q, K (and V): a table
  *      of the largest key norm of every 64-key tile, which bounds every score
  *      so that most tiles skip their row maximum, tables of the largest key
@@ -102,12 +102,12 @@ int sah_causal_attention_bsd(
     void* workspace, size_t workspace_bytes,
     sah_stream_t stream);
 
-/* Workspace bytes sah_causal_attention_bsd needs: for seq_len >= 16384 the
+/* Workspace bytes sah_causal_attention_bsd needs: for seq_len >= 4096 the
  * key-norm table (4 bytes per 64-key tile per head, rounded up to 256), the
  * key and query block-norm tables (8 bytes per 512-row block per head,
  * rounded up to 256) and the fp16 scaled keys (128 bytes per key, seq_len
  * rounded up to 64, per head), then V^T when value is head_dim-contiguous;
- * 0 for a seq-contiguous value shorter than 16384 keys. */
+ * 0 for a seq-contiguous value shorter than 4096 keys. */
 size_t sah_causal_attention_workspace_bytes(
     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
     int64_t v_stride_s, int64_t v_stride_d, int dtype);

@@ -66,12 +66,14 @@ constexpr float kScaledKeyMaxNorm = 4096.0f;
 // of the keys it reads, so every launch takes the same path for a row and the
 // results stay independent of the launch.
 constexpr int kScaledKeyRows = 512;
-// Sequences at least this long get the key-norm pre-pass (one extra read of
-// K).  Measured on MI355X, bf16, pre-pass included: 40.51 -> 38.93 ms on the
-// long-sequence chunk (B2 H16 S100000), 0.645 -> 0.633 ms at B1 H16 S16384,
-// but 1.53 -> 1.57 ms at B16 H32 S4096 and 0.101 -> 0.112 ms at B8 H16 S2048,
-// where the pre-pass costs more than the skipped maxima save.
-constexpr int64_t kKeyNormMinSeq = 16384;
+// Sequences at least this long get the preparation launch (norm tables and
+// fp16 scaled keys, one extra read of Q and K) and with it the scaled-key
+// path.  Measured on MI355X, bf16, preparation included, same box with the
+// two thresholds alternating: the C4 forward (B16 H32 S4096, two layers)
+// 13.11/13.13 -> 12.92/12.96 ms with the path from 4096 keys on; at B8 H16
+// S2048 the attention operator 82.3 -> 99.4 us, where the preparation costs
+// more than the cheaper tiles save.
+constexpr int64_t kKeyNormMinSeq = 4096;
 
 struct AttnParams {
   const void* q;

@@ -313,7 +313,7 @@ def test_score_bound_path_sampled_rows(gpu_device, case):
 
 
 def test_fp16_score_bound_keeps_probabilities_in_range(gpu_device):
-    """fp16 P overflows above 65504: on the score-bound path (S >= 16384) an
+    """fp16 P overflows above 65504: on the score-bound path (S >= 4096) an
     fp16 row may skip its tile maximum only while its bound keeps every
     probability below 2^15.  Key 15000 is set to 3.8 x query 15005, so that
     row's score for it is about 40 powers of two above its shift while the

@@ -142,7 +142,7 @@ def test_long_sequence_every_row_matches_the_portable_program(gpu_device):
     assert reference_signature["attention_backend"] != "hip_streaming_dh64", reference_signature
     assert bool(torch.isfinite(output).all())
     _assert_model(exact, reference_path, output, "C5 S=100000 all rows vs portable program")
-    # the late rows (past 16384 keys the attention runs its score-bound path)
+    # the late rows, whose 512-row blocks read the most keys
     late = slice(seq - 4096, seq)
     _assert_model(exact[:, late], reference_path[:, late], output[:, late], "C5 last 4096 rows")
     # the prefix against the CPU oracle: rows < 2048 see only keys < 2048

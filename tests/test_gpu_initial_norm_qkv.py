@@ -188,7 +188,7 @@ def test_fused_initial_norm_plan_equals_the_unfused_plan(gpu_device, shape):
 
 def test_streamed_long_sequence_with_the_fused_initial_norm(gpu_device):
     """The streamed long-sequence program (one sequence per microbatch, past
-    the attention's 16384-key score-bound threshold) with the fused initial
+    the attention's 4096-key score-bound threshold) with the fused initial
     norm equals the same program with the separate norm kernel."""
 
     from solution.config import InitialNormBackend, QKVMaterialization

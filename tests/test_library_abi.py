@@ -75,6 +75,9 @@ def test_host_only_entry_points():
     assert library.sah_causal_attention_workspace_bytes(1, 16, 16384, 64, 1, 16384, 1) == (
         16 * 256 * 4 + 2 * 16 * 32 * 4 + 16 * 16384 * 128
     )
+    # The tables and scaled keys start at 4096 keys.
+    assert library.sah_causal_attention_workspace_bytes(1, 2, 4096, 64, 1, 4096, 2) == 512 + 256 + 2 * 4096 * 128
+    assert library.sah_causal_attention_workspace_bytes(1, 2, 4095, 64, 1, 4096, 2) == 0
     # Shorter sequences need only the V^T buffer, and seq-contiguous V none.
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 64, 1, 2) == 8 * 16 * 64 * 2048 * 2
     assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 1, 2048, 2) == 0
