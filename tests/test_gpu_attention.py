@@ -366,6 +366,30 @@ def test_scaled_key_path_sampled_rows(gpu_device, dtype, magnitude):
         _assert_parity(torch.from_numpy(expected).float(), actual, dtype, f"scaled keys head {head}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seq", [4095, 4096, 4097])
+def test_preparation_threshold_boundary(gpu_device, dtype, seq):
+    """4095 keys run the transpose and the shifted path, 4096 and more the
+    preparation launch and the scaled-key path (the workspace holds the norm
+    tables and scaled keys only then).  Every row on both sides of the
+    boundary against the fp32 oracle, under the 8-wave ring launch and a
+    4-wave launch."""
+
+    from solution.kernels.hip import _library
+
+    library = _library.load_library()
+    code = 1 if dtype == torch.float16 else 2
+    v_only = 2 * 64 * (-(-seq // 64) * 64) * 2
+    workspace = library.sah_causal_attention_workspace_bytes(1, 2, seq, 64, 64, 1, code)
+    assert (workspace > v_only) == (seq >= 4096), (seq, workspace, v_only)
+    q, k, v = _inputs(1, 2, seq, dtype=dtype, seed=seq)
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    for block_m, warps in ((256, 8), (128, 4)):
+        print(f"threshold boundary dtype={dtype} S={seq} launch=({block_m}, {warps}, 2)", flush=True)
+        output = _run(q, k, v, gpu_device, block_m=block_m, num_warps=warps, num_stages=2)
+        _assert_parity(reference, output, dtype, f"S={seq} launch ({block_m}, {warps})")
+
+
 def test_scaled_keys_in_the_workspace(gpu_device):
     """The preparation launch writes the largest |k| of every 64-key tile,
     then the largest |k| and the largest |q| of every 512-row block, then
