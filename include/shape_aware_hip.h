@@ -102,12 +102,13 @@ int sah_causal_attention_bsd(
     void* workspace, size_t workspace_bytes,
     sah_stream_t stream);
 
-/* Workspace bytes sah_causal_attention_bsd needs: for seq_len >= 4096 the
- * key-norm table (4 bytes per 64-key tile per head, rounded up to 256), the
- * key and query block-norm tables (8 bytes per 512-row block per head,
- * rounded up to 256) and the fp16 scaled keys (128 bytes per key, seq_len
- * rounded up to 64, per head), then V^T when value is head_dim-contiguous;
- * 0 for a seq-contiguous value shorter than 4096 keys. */
+/* Workspace bytes sah_causal_attention_bsd needs (the most over its
+ * launches): for seq_len >= 4096 the key-norm table (4 bytes per 64-key tile
+ * per head, rounded up to 256), the key and query block-norm tables (8 bytes
+ * per 512-row block per head, rounded up to 256) and the fp16 scaled keys
+ * (128 bytes per key, seq_len rounded up to 64, per head), then V^T when value
+ * is head_dim-contiguous; 0 for a seq-contiguous value shorter than 4096 keys.
+ * The pipelined launch (num_stages 3) uses only the V^T region. */
 size_t sah_causal_attention_workspace_bytes(
     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
     int64_t v_stride_s, int64_t v_stride_d, int dtype);
@@ -121,11 +122,19 @@ size_t sah_causal_attention_workspace_bytes(
  * allocation.  Arguments are those of sah_causal_attention_bsd without the
  * workspace pair: the workspace is a static device array of
  * SAH_ATTENTION_STATIC_WORKSPACE_BYTES (64 MiB) that each GPU holds for the
- * life of the process.  A call whose sah_causal_attention_workspace_bytes()
- * exceeds that returns SAH_ERR_WORKSPACE before any launch (for example V in
- * the reference [B, H, S, 64] layout needs B*H*64*roundup(S, 64)*2 bytes, so
- * B8 H16 S2048 fits and one 2 x 100000-token chunk does not; a seq-contiguous
- * V needs only the norm tables and the scaled keys).  All calls on one GPU share its array:
+ * life of the process.  From 4096 keys a call takes the prepared layout of
+ * sah_causal_attention_bsd (norm tables, fp16 scaled keys, then V^T for a
+ * head_dim-contiguous V) when it fits the array, with bitwise the same
+ * result.  When it does not fit (for example BASELINE C4's B16 H32 S4096:
+ * 268 MB of scaled keys), the call runs every workgroup on the plain kernel's
+ * shifted path without the preparation launch, as below 4096 keys; that
+ * needs only V^T for a head_dim-contiguous V (B*H*64*roundup(S, 64)*2 bytes)
+ * and nothing for a seq-contiguous V, and its result agrees with
+ * sah_causal_attention_bsd's to the 16-bit tolerance, not bitwise.  The
+ * pipelined launch (num_stages 3) needs only V^T.  A call whose V^T alone
+ * exceeds the array returns SAH_ERR_WORKSPACE before any launch (B8 H16 S2048
+ * fits; one 2 x 100000-token chunk with V in [B, H, S, 64] does not).  All
+ * calls on one GPU share its array:
  * calls that may overlap on that GPU (different streams, or host threads)
  * race on it and must be serialized by the caller.  Nothing in it needs to
  * start at zero; every call writes what it reads.

@@ -867,6 +867,47 @@ size_t scaled_key_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
   return (size_t)batch * (size_t)heads * (size_t)padded_seq(seq_len) * kHeadDim * sizeof(f16);
 }
 
+// The regions of one call's workspace, in order: the three norm tables and
+// the fp16 scaled keys when the call runs the preparation launch, then V^T
+// when V is head_dim-contiguous.
+struct WorkspaceLayout {
+  size_t norm = 0, block = 0, kc = 0, vt = 0;
+  size_t total() const { return norm + block + kc + vt; }
+};
+
+// `prepared`: the call runs the preparation launch (long sequences on the
+// plain kernel).  Without it the plain kernel takes the shifted path for
+// every workgroup, as below 4096 keys, and needs no tables.
+WorkspaceLayout workspace_layout(int64_t batch, int64_t heads, int64_t seq_len,
+                                 int64_t v_stride_d, int dtype, bool prepared) {
+  WorkspaceLayout layout;
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || dtype == SAH_DTYPE_F32) return layout;
+  if (prepared) {
+    layout.norm = key_norm_bytes(batch, heads, seq_len);
+    layout.block = row_block_bytes(batch, heads, seq_len);
+    layout.kc = scaled_key_bytes(batch, heads, seq_len);
+  }
+  if (v_stride_d == 1)
+    layout.vt = (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
+  return layout;
+}
+
+// Whether a call may run the preparation launch: a long sequence on the
+// plain kernel (the pipelined kernel, num_stages 3, keeps the exact running
+// maximum and never reads the tables).
+bool prepares(int64_t seq_len, int num_stages, int dtype) {
+  return seq_len >= kKeyNormMinSeq && num_stages != 3 && dtype != SAH_DTYPE_F32;
+}
+
+int run_attention(
+    const void* query, const void* key, const void* value, void* output, int64_t batch,
+    int64_t heads, int64_t seq_len, int64_t head_dim, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages, void* workspace,
+    size_t workspace_bytes, bool allow_prepare, hipStream_t stream);
+
 }  // namespace
 }  // namespace sah
 
@@ -883,13 +924,10 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
                                                        int64_t v_stride_d, int dtype) {
   (void)head_dim;
   (void)v_stride_s;
-  if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;
-  if (dtype == SAH_DTYPE_F32) return 0;  // the fp32 kernel reads K and V as given
-  const size_t table = key_norm_bytes(batch, heads, seq_len) +
-                       row_block_bytes(batch, heads, seq_len) +
-                       scaled_key_bytes(batch, heads, seq_len);
-  if (v_stride_d != 1) return table;  // V already seq-contiguous (V^T storage)
-  return table + (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
+  // The largest need over the launches: the pipelined launch (num_stages 3)
+  // needs only the V^T region.  The fp32 kernel reads K and V as given.
+  return workspace_layout(batch, heads, seq_len, v_stride_d, dtype,
+                          prepares(seq_len, 2, dtype)).total();
 }
 
 extern "C" int sah_causal_attention_bsd(
@@ -900,7 +938,24 @@ extern "C" int sah_causal_attention_bsd(
     int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
     int block_m, int block_n, int num_warps, int num_stages, void* workspace,
     size_t workspace_bytes, sah_stream_t stream_handle) {
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+  return run_attention(query, key, value, output, batch, heads, seq_len, head_dim, q_stride_b,
+                       q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s, v_stride_b,
+                       v_stride_h, v_stride_s, v_stride_d, o_stride_b, o_stride_s, scale, dtype,
+                       block_m, block_n, num_warps, num_stages, workspace, workspace_bytes,
+                       /*allow_prepare=*/true, reinterpret_cast<hipStream_t>(stream_handle));
+}
+
+namespace sah {
+namespace {
+
+int run_attention(
+    const void* query, const void* key, const void* value, void* output, int64_t batch,
+    int64_t heads, int64_t seq_len, int64_t head_dim, int64_t q_stride_b,
+    int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
+    int block_m, int block_n, int num_warps, int num_stages, void* workspace,
+    size_t workspace_bytes, bool allow_prepare, hipStream_t stream) {
   if (query == nullptr || key == nullptr || value == nullptr || output == nullptr)
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention tensors must be non-null");
   if (head_dim != kHeadDim)
@@ -1007,20 +1062,22 @@ extern "C" int sah_causal_attention_bsd(
   prm.num_blocks = (int)blocks;
 
   // Workspace: the per-tile key-norm table, the per-block key and query norm
-  // tables and the fp16 scaled keys (long sequences), then (reference V
-  // layout only) V^T.
-  const size_t need = sah_causal_attention_workspace_bytes(
-      batch, heads, seq_len, head_dim, v_stride_s, v_stride_d, dtype);
+  // tables and the fp16 scaled keys (long sequences on the plain kernel),
+  // then (reference V layout only) V^T.
+  const bool prepared = allow_prepare && prepares(seq_len, num_stages, dtype);
+  const WorkspaceLayout layout =
+      workspace_layout(batch, heads, seq_len, v_stride_d, dtype, prepared);
+  const size_t need = layout.total();
   if (need > 0 && (workspace == nullptr || workspace_bytes < need))
     return fail(SAH_ERR_WORKSPACE, "attention needs %zu workspace bytes, got %zu", need,
                 workspace_bytes);
   if (need > 0 && !aligned16(workspace))
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention workspace must be 16-byte aligned");
-  const size_t norm_bytes = key_norm_bytes(batch, heads, seq_len);
-  const size_t block_bytes = row_block_bytes(batch, heads, seq_len);
-  const size_t kc_bytes = scaled_key_bytes(batch, heads, seq_len);
+  const size_t norm_bytes = layout.norm;
+  const size_t block_bytes = layout.block;
+  const size_t kc_bytes = layout.kc;
   unsigned char* base = static_cast<unsigned char*>(workspace);
-  void* vt_space = need > 0 ? base + norm_bytes + block_bytes + kc_bytes : nullptr;
+  void* vt_space = layout.vt > 0 ? base + norm_bytes + block_bytes + kc_bytes : nullptr;
   const int64_t seq_pad = padded_seq(seq_len);
   int status = SAH_OK;
   prm.knorm = nullptr;
@@ -1051,9 +1108,6 @@ extern "C" int sah_causal_attention_bsd(
                 "key/value row strides must lie in [0, 2^24) elements (32-bit tile offsets)");
   // Long sequences (the plain kernel): one preparation launch writes the
   // norm tables, the fp16 scaled keys and, for a head_dim-contiguous V, V^T.
-  // The pipelined kernel (num_stages 3) keeps the exact running maximum and
-  // never reads the tables; their regions of the workspace then stay unused.
-  const bool prepared = norm_bytes > 0 && num_stages != 3;
   if (prepared) {
     PrepParams pp;
     pp.k = key;
@@ -1114,11 +1168,15 @@ extern "C" int sah_causal_attention_bsd(
              : launch_attention<f16>(prm, block_m, num_warps, num_stages, stream);
 }
 
+}  // namespace
+}  // namespace sah
+
 // ---------------------------------------------------------------------------
 // Variant of sah_causal_attention_bsd for callers that cannot allocate
 // device memory (code under HIP graph capture, tight serving loops): the
-// workspace (key-norm table and V^T staging) lives in this file-scope device
-// array, of which each GPU holds its own copy for the life of the process.
+// workspace (norm tables, fp16 scaled keys, V^T staging) lives in this
+// file-scope device array, of which each GPU holds its own copy for the life
+// of the process.
 // Kernel arguments need its device address, which differs per GPU and is
 // looked up once per device with hipGetSymbolAddress; the array's name is
 // only a host-side stand-in and is never passed to a kernel.
@@ -1160,23 +1218,25 @@ extern "C" int sah_causal_attention_bsd_static_workspace(
     int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
     int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
     int block_m, int block_n, int num_warps, int num_stages, sah_stream_t stream) {
-  const size_t need = sah_causal_attention_workspace_bytes(batch, heads, seq_len, head_dim,
-                                                           v_stride_s, v_stride_d, dtype);
-  if (need > (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES)
+  // The prepared layout when it fits the array; otherwise the plain kernel's
+  // shifted path for every workgroup, which needs at most the V^T region.
+  constexpr size_t kLimit = (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES;
+  const bool prepare = prepares(seq_len, num_stages, dtype) &&
+                       workspace_layout(batch, heads, seq_len, v_stride_d, dtype, true).total() <= kLimit;
+  const size_t need = workspace_layout(batch, heads, seq_len, v_stride_d, dtype, prepare).total();
+  if (need > kLimit)
     return fail(SAH_ERR_WORKSPACE,
                 "attention needs %zu workspace bytes, above the static workspace of %zu bytes; "
                 "use sah_causal_attention_bsd with a caller-provided workspace",
-                need, (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES);
+                need, kLimit);
   void* workspace = nullptr;
   if (need > 0) {
     workspace = scratch_address();
     if (workspace == nullptr) return SAH_ERR_HIP;
   }
-  return sah_causal_attention_bsd(query, key, value, output, batch, heads, seq_len, head_dim,
-                                  q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h,
-                                  k_stride_s, v_stride_b, v_stride_h, v_stride_s, v_stride_d,
-                                  o_stride_b, o_stride_s, scale, dtype, block_m, block_n,
-                                  num_warps, num_stages, workspace,
-                                  need > 0 ? (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES : 0,
-                                  stream);
+  return run_attention(query, key, value, output, batch, heads, seq_len, head_dim, q_stride_b,
+                       q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s, v_stride_b,
+                       v_stride_h, v_stride_s, v_stride_d, o_stride_b, o_stride_s, scale, dtype,
+                       block_m, block_n, num_warps, num_stages, workspace, need > 0 ? kLimit : 0,
+                       prepare, reinterpret_cast<hipStream_t>(stream));
 }

@@ -1,9 +1,14 @@
 """sah_causal_attention_bsd_static_workspace, the attention entry point that
 allocates nothing (its workspace is a static device array), against
-sah_causal_attention_bsd with a caller-provided workspace: the same kernels,
-so the outputs must be bitwise equal.  Each case makes two calls in a row,
-the second on a smaller input, so the second reads the array the first left
-behind.  Both entry points are called through the C ABI (ctypes)."""
+sah_causal_attention_bsd with a caller-provided workspace.  Where the
+prepared long-sequence layout (norm tables, fp16 scaled keys, V^T) fits the
+array, both run the same kernels and the outputs must be bitwise equal.
+Where it does not, the static entry runs every workgroup on the plain
+kernel's shifted path (no preparation, at most the V^T region), and the
+outputs must agree to the bf16/fp16 gate (|err| <= 2e-2 or |err| <= 1e-2
+|ref|).  Each case makes two calls in a row, the second on a smaller input,
+so the second reads the array the first left behind.  Both entry points are
+called through the C ABI (ctypes)."""
 
 from __future__ import annotations
 
@@ -56,6 +61,18 @@ CASES = [
     (torch.bfloat16, False, (128, 64, 4, 3), (1, 4, 17000), (1, 2, 333)),
 ]
 
+# Calls whose prepared layout exceeds the static array: the static entry runs
+# the shifted path without preparation.  (dtype, seq-contiguous V, launch,
+# first, second smaller)
+FALLBACK_CASES = [
+    # BASELINE C4's attention (B16 H32 S4096) with V seq-contiguous: the
+    # scaled keys alone are 268 MB; the shifted path needs no workspace.
+    (torch.bfloat16, True, (256, 64, 8, 2), (16, 32, 4096), (2, 16, 4500)),
+    # V in [B, H, S, 64]: tables + scaled keys + V^T just over 64 MiB, V^T
+    # alone (33.5 MB) fits.
+    (torch.bfloat16, False, (256, 64, 8, 2), (1, 16, 16384), (1, 8, 5000)),
+]
+
 
 def test_header_states_the_static_workspace_size():
     from solution.kernels.hip import _library
@@ -80,6 +97,36 @@ def test_static_workspace_matches_caller_workspace(gpu_device, dtype, seq_major_
         torch.cuda.synchronize(gpu_device)
         assert bool(torch.isfinite(got).all())
         assert torch.equal(got, want), f"call {index} {shape}: outputs differ"
+
+
+@pytest.mark.parametrize("dtype,seq_major_v,launch,first,second", FALLBACK_CASES)
+def test_static_workspace_runs_unprepared_when_the_prepared_layout_does_not_fit(
+    gpu_device, dtype, seq_major_v, launch, first, second
+):
+    from oracle.compare import parity_gate
+    from solution.kernels.hip._library import ATTENTION_STATIC_WORKSPACE_BYTES, dtype_code, load_library, stream_handle
+
+    library = load_library()
+    stream = stream_handle(gpu_device)
+    batch, heads, seq = first
+    # the caller-workspace need is the prepared layout's (num_stages 2)
+    v_stride_s, v_stride_d = (1, seq) if seq_major_v else (64, 1)
+    prepared = library.sah_causal_attention_workspace_bytes(
+        batch, heads, seq, 64, v_stride_s, v_stride_d, dtype_code(dtype))
+    assert prepared > ATTENTION_STATIC_WORKSPACE_BYTES
+    for index, shape in enumerate((first, second)):
+        print(f"static workspace fallback dtype={dtype} seq_major_v={seq_major_v} launch={launch} "
+              f"call={index} shape={shape}", flush=True)
+        q, k, v = _inputs(*shape, dtype, 200 + index, seq_major_v, gpu_device)
+        assert (v.stride(2) == 1) == seq_major_v
+        want = _call(library, False, q, k, v, launch, 0.125, dtype_code(dtype), stream)
+        got = _call(library, True, q, k, v, launch, 0.125, dtype_code(dtype), stream)
+        torch.cuda.synchronize(gpu_device)
+        assert bool(torch.isfinite(got).all())
+        result = parity_gate(want.float().cpu(), got.float().cpu(), dtype)
+        print(f"  vs caller workspace: max_abs={result.max_abs_error:.3g} failed={result.failed_elements}",
+              flush=True)
+        assert result.passed, f"call {index} {shape}: {result}"
 
 
 def test_requests_beyond_the_static_workspace_are_rejected_before_launch(gpu_device):
