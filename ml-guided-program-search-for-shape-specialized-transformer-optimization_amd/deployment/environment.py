@@ -6,9 +6,13 @@ the same JSON field names, the canonical SHA-256 ``identity`` and the
 the fields are ROCm's instead of CUDA's:
 
   compute_capability    gcnArchName, e.g. "gfx950:sramecc+:xnack-"
-  driver_version        amdgpu kernel driver (/sys/module/amdgpu/version,
-                        else the ROCm SMI library), replacing the nvidia-smi
-                        probe of the reference (:99-124)
+  driver_version        amdgpu kernel driver: the module's own version where
+                        amdgpu is a loadable module (/sys/module/amdgpu/
+                        version, e.g. a DKMS build), else the upstream release
+                        of the kernel that carries it (the leading
+                        major.minor.patch that ROCm SMI or uname reports),
+                        replacing the nvidia-smi probe of the reference
+                        (:99-124)
   cuda_runtime_version  torch.version.hip (the HIP runtime torch ships)
   cudnn_version         MIOpen version as torch reports it
 """
@@ -18,6 +22,8 @@ from __future__ import annotations
 import hashlib
 import importlib.metadata
 import json
+import platform
+import re
 import subprocess
 from dataclasses import dataclass
 from enum import Enum
@@ -106,8 +112,23 @@ def solution_implementation_digest(
     return _files_digest(root, paths)
 
 
+_KERNEL_RELEASE = re.compile(r"^(\d+\.\d+(?:\.\d+)?)")
+
+
+def kernel_driver_release(release: str) -> str | None:
+    """The upstream part of a kernel release string ("6.18.44" of
+    "6.18.44-fc-v1045-amdproxy9"), or None when it does not start with one.
+    The suffix names the distribution's build of the host kernel; machines of
+    one pool run the same driver under different suffixes."""
+
+    match = _KERNEL_RELEASE.match(release.strip())
+    return match.group(1) if match else None
+
+
 def amdgpu_driver_version() -> str:
-    """Version of the amdgpu kernel driver."""
+    """Version of the amdgpu kernel driver: the loadable module's version
+    when sysfs has it, else the upstream release of the kernel the driver is
+    built into (as ROCm SMI reports it on such systems, or uname)."""
 
     sysfs = Path("/sys/module/amdgpu/version")
     try:
@@ -116,6 +137,7 @@ def amdgpu_driver_version() -> str:
             return text
     except OSError:
         pass
+    reported: str | None = None
     try:
         completed = subprocess.run(
             ["rocm-smi", "--showdriverversion", "--json"],
@@ -126,9 +148,15 @@ def amdgpu_driver_version() -> str:
             if isinstance(value, dict):
                 for key, item in value.items():
                     if "driver" in key.lower():
-                        return str(item)
+                        reported = str(item)
+                        break
+            if reported is not None:
+                break
     except (OSError, subprocess.SubprocessError, ValueError):
         pass
+    for candidate in (reported, platform.release()):
+        if candidate:
+            return kernel_driver_release(candidate) or candidate
     raise RuntimeError("cannot determine the amdgpu driver version")
 
 
@@ -264,6 +292,7 @@ __all__ = [
     "amdgpu_driver_version",
     "configure_process_math_mode",
     "installed_triton_version",
+    "kernel_driver_release",
     "official_definitions_digest",
     "solution_implementation_digest",
     "stable_digest",

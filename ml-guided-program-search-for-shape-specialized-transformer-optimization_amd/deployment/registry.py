@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import json
 import os
+import stat
 import tempfile
 from dataclasses import astuple, dataclass, fields
 from pathlib import Path
@@ -171,11 +172,36 @@ class RegistryIndex:
         try:
             with os.fdopen(handle, "w", encoding="utf-8") as stream:
                 stream.write(text)
+            # mkstemp creates the file 0600; the published file keeps the
+            # mode of the one it replaces, or a new file's default (0666 less
+            # the umask), so readers under other uids still read it.
+            os.chmod(temporary, _published_mode(target))
             os.replace(temporary, target)
         except BaseException:
             Path(temporary).unlink(missing_ok=True)
             raise
         return target
+
+
+def _process_umask() -> int:
+    # Read from /proc where it exists: setting and restoring os.umask would
+    # briefly change it for every thread of the process.
+    try:
+        for line in Path("/proc/self/status").read_text(encoding="ascii").splitlines():
+            if line.startswith("Umask:"):
+                return int(line.split()[1], 8)
+    except (OSError, ValueError):
+        pass
+    umask = os.umask(0o022)
+    os.umask(umask)
+    return umask
+
+
+def _published_mode(target: Path) -> int:
+    try:
+        return stat.S_IMODE(target.stat().st_mode)
+    except FileNotFoundError:
+        return 0o666 & ~_process_umask()
 
 
 def _fingerprint(hardware: EnvironmentFingerprint | dict[str, Any]) -> EnvironmentFingerprint:

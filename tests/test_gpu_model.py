@@ -429,16 +429,33 @@ def test_default_resolution_selects_the_published_registry_entry(gpu_device):
     from deployment.environment import EnvironmentFingerprint, ImplementationScope
     from deployment.registry import ShapeFingerprint, resolve_deployed_config
 
+    import json
+
+    from deployment.registry import DEFAULT_DEPLOYED_CONFIGS_PATH
+
     config = TransformerConfig(64, 256, 512, 8, 2048, 4, True)
+    detected = EnvironmentFingerprint.detect(gpu_device, scope=ImplementationScope.RESIDENT)
     published = resolve_deployed_config(
-        hardware=EnvironmentFingerprint.detect(gpu_device, scope=ImplementationScope.RESIDENT),
+        hardware=detected,
         shape=ShapeFingerprint(
             batch_size=64, qkv_dim=512, heads=8, seq_len=256, layers=4, causal=True, ffn_dim=2048,
             dtype="bfloat16", padding_ratio=0.0, input_scale=1.0,
         ),
     )
     if published is None:
-        pytest.skip("the registry holds no entry for this environment's fingerprint")
+        # name the fields that keep every committed bundle from matching
+        document = json.loads(DEFAULT_DEPLOYED_CONFIGS_PATH.read_text(encoding="utf-8"))
+        mine = detected.to_dict()
+        for bundle in document["bundles"]:
+            theirs = bundle["hardware"]
+            differing = {
+                key: (theirs.get(key), mine[key])
+                for key in mine
+                if key not in ("official_definitions_digest", "solution_implementation_digest")
+                and theirs.get(key) != mine[key]
+            }
+            print(f"bundle {theirs.get('scope')}: fields differing (committed, detected): {differing}", flush=True)
+    assert published is not None, "the committed registry holds no entry for this environment's fingerprint"
     model = _model(config, xavier_init_weights(config, seed=3), gpu_device, torch.bfloat16)
     x = generate_input(config, seed=3).to(torch.bfloat16).to(gpu_device)
     with torch.inference_mode():

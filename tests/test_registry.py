@@ -122,3 +122,43 @@ def test_other_schema_versions_and_malformed_files(tmp_path):
     path.write_text("[1, 2]", encoding="utf-8")
     with pytest.raises(ValueError):
         RegistryIndex.read(path)
+
+
+def test_publish_keeps_the_file_mode(tmp_path):
+    """The atomic rewrite keeps the replaced file's mode (mkstemp's 0600 would
+    lock out readers under other uids); a new file gets 0666 less the umask."""
+
+    import os
+    import stat
+
+    path = tmp_path / "registry.json"
+    path.write_text(json.dumps(COMMITTED), encoding="utf-8")
+    os.chmod(path, 0o644)
+    publish_deployed_config(hardware=_hardware(), shape=SHAPE, config=hip_config(), path=path)
+    assert stat.S_IMODE(path.stat().st_mode) == 0o644
+    os.chmod(path, 0o664)
+    publish_deployed_config(hardware=_hardware(), shape=SHAPE, config=hip_config(microbatch_size=2), path=path)
+    assert stat.S_IMODE(path.stat().st_mode) == 0o664
+    fresh = tmp_path / "fresh.json"
+    umask = os.umask(0o022)
+    try:
+        publish_deployed_config(hardware=_hardware(), shape=SHAPE, config=hip_config(), path=fresh)
+    finally:
+        os.umask(umask)
+    assert stat.S_IMODE(fresh.stat().st_mode) == 0o644
+
+
+def test_driver_version_is_the_kernel_release_without_its_build_suffix():
+    """Boxes of one pool run one amdgpu driver under kernel releases that
+    differ only in the distribution's build suffix; the fingerprint keeps the
+    upstream release, so a measurement published on one box serves the others."""
+
+    from deployment.environment import kernel_driver_release
+
+    assert kernel_driver_release("6.18.44-fc-v1045-amdproxy9") == "6.18.44"
+    assert kernel_driver_release("6.18.44-fc-v595-amdproxy8") == "6.18.44"
+    assert kernel_driver_release("6.8.0-45-generic") == "6.8.0"
+    assert kernel_driver_release("6.10") == "6.10"
+    assert kernel_driver_release("unknown") is None
+    for bundle in COMMITTED["bundles"]:
+        assert bundle["hardware"]["driver_version"] == kernel_driver_release(bundle["hardware"]["driver_version"])
