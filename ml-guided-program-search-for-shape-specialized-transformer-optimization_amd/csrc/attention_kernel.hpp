@@ -48,11 +48,16 @@ constexpr float safe_exponent() {
 // such score lies in [-bound, bound], P = exp2(score) needs neither a shift
 // nor a row maximum (bf16 P: 2^32 is far inside the fp32 exponent range; fp16
 // P: 2^15 < 65504).  Softmax is shift-invariant; only the point where P is
-// rounded to 16 bits moves, and the relative rounding error of P is the same
-// at any exponent.  The fp16 key product adds at most 2^-12 relative per term,
-// under a quarter of a bf16 ulp of P at the bound.  Blocks with a larger
-// bound (large-magnitude inputs, an outlier key or query) keep the shifted
-// path on the original keys.
+// rounded to 16 bits moves.  Rounding P to bf16 has the same relative error at
+// any exponent; fp16 P below 2^-14 is subnormal and keeps an absolute error
+// of 2^-25, at most 2^-10 relative at the smallest P of 2^-15.  Rounding c k
+// to fp16 (unit roundoff 2^-11) moves a score by at most 2^-11 c |q| |k| in
+// log2 units: 2^-6 at the bf16 bound, up to 1.1% on one P when the 64
+// roundings of a key all lean the same way against q, about 0.1% for
+// roundings of random sign.  The official bf16 order rounds the score itself
+// to bf16 (2^-9 relative), four times that bound at the same scores.
+// Blocks with a larger bound (large-magnitude inputs, an outlier key or
+// query) keep the shifted path on the original keys.
 template <typename T>
 constexpr float scaled_key_bound() {
   return std::is_same<T, f16>::value ? 15.0f : 32.0f;

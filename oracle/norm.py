@@ -3,11 +3,12 @@
 residual_layer_norm follows the reference's same-dtype boundary:
 ``residual_add`` (solution/operators/norm/residual_add.py:28-39: value + update
 in the stream dtype) followed by ``nn.LayerNorm`` (biased variance, eps 1e-5;
-solution/transformer.py:1629-1632).  mixed_residual_layer_norm follows
-solution/kernels/norm/triton_mixed_residual.py:41-76 (fp32 stream, 16-bit
-update promoted to fp32, normalized output 16-bit or fp32 at the final
-boundary).  The statistics are computed in float64 here, so the oracle is at
-least as accurate as any fp32 kernel it checks.
+solution/transformer.py:1629-1632).  The same function covers the mixed
+boundary of solution/kernels/norm/triton_mixed_residual.py:41-76 (an fp32
+stream with a 16-bit update, promoted exactly; normalized output 16-bit, or
+fp32 at the final boundary) through its ``normalized_dtype``.  The statistics
+are computed in float64 here, so the oracle is at least as accurate as any
+fp32 kernel it checks.
 """
 
 from __future__ import annotations

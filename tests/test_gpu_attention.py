@@ -366,6 +366,60 @@ def test_scaled_key_path_sampled_rows(gpu_device, dtype, magnitude):
         _assert_parity(torch.from_numpy(expected).float(), actual, dtype, f"scaled keys head {head}")
 
 
+@pytest.mark.parametrize("dtype,bound,limit", [(torch.bfloat16, 31.0, 32.0), (torch.float16, 14.5, 15.0)])
+@pytest.mark.parametrize("value_scale", [1.0, 4.0])
+def test_scaled_key_path_near_its_bound_with_aligned_rows(gpu_device, dtype, bound, limit, value_scale):
+    """Queries and keys that share one direction (q nearly parallel to many
+    keys), scaled so that c max|q| max|k| sits just under the scaled-key limit
+    (32 for bf16 P, 15 for fp16 P): every 512-row block takes the scaled-key
+    path with scores close to the limit, where the fp16 rounding of c k
+    (unit roundoff 2^-11) weighs most.  Sampled rows against float64 per-row
+    math: with V of magnitude 1 at the gate; with V of magnitude 4, where
+    rounding P to 16 bits before PV (the reference's order) alone moves a
+    near-one-hot row by more than 2e-2, no less accurate than the official
+    order in the same dtype (scores, softmax cast and PV as
+    official/torch_transformer_benchmark.py:97-112)."""
+
+    seq, heads = 4608, 2
+    c = 0.125 * math.log2(math.e)
+    generator = torch.Generator().manual_seed(17)
+    direction = torch.randn(64, generator=generator)
+    direction /= direction.norm()
+
+    def aligned():
+        noise = torch.randn(1, heads, seq, 64, generator=generator) * 0.5
+        along = torch.randn(1, heads, seq, 1, generator=generator) * 3.0
+        return noise + along * direction
+
+    k = aligned().to(dtype)
+    q = aligned()
+    factor = bound / (c * q.norm(dim=-1).max() * k.float().norm(dim=-1).max())
+    q = (q * factor).to(dtype)
+    reach = c * q.float().norm(dim=-1).max() * k.float().norm(dim=-1).max()
+    # within the scaled-key limit (the 16-bit rounding of q moves it a little)
+    assert bound - 1.0 < float(reach) < limit, float(reach)
+    v = (torch.randn(1, heads, seq, 64, generator=generator) * value_scale).to(dtype)
+    print(f"scaled-key bound {dtype} reach={float(reach):.2f} |v|x{value_scale}", flush=True)
+    output = _run(q, k, v, gpu_device, block_m=256, num_warps=8, num_stages=2).float().cpu()
+    official = _to_bsd(query_block_causal_attention(q, k, v, 1 / 8)).float()
+    rng = np.random.default_rng(5)
+    rows = np.unique(np.concatenate([np.arange(0, 8), np.arange(seq - 8, seq), rng.integers(0, seq, 48)]))
+    for head in range(heads):
+        expected = torch.from_numpy(causal_attention_rows(
+            q[0, head].float().numpy(), k[0, head].float().numpy(), v[0, head].float().numpy(), rows, 1 / 8
+        )).float()
+        columns = slice(head * 64, (head + 1) * 64)
+        result = parity_gate(expected, output[0, rows, columns], dtype)
+        order = parity_gate(expected, official[0, rows, columns], dtype)
+        print(f"  head {head}: HIP max_abs={result.max_abs_error:.3g} failed={result.failed_elements}; "
+              f"official order max_abs={order.max_abs_error:.3g} failed={order.failed_elements}", flush=True)
+        if value_scale == 1.0:
+            _assert_parity(expected, output[0, rows, columns], dtype, f"aligned rows head {head}")
+        else:
+            assert result.failed_elements <= order.failed_elements + 1, (result, order)
+            assert result.max_abs_error <= max(2e-2, 1.25 * order.max_abs_error), (result, order)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("seq", [4095, 4096, 4097])
 def test_preparation_threshold_boundary(gpu_device, dtype, seq):

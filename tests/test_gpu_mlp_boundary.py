@@ -200,3 +200,47 @@ def test_fused_mlp_program_matches_the_oracle(gpu_device, shape):
     parity = model_parity(exact, reference_path, output.float().cpu())
     print(f"fused MLP model {shape}: {parity.summary()}", flush=True)
     assert parity.passed, parity.summary()
+
+
+@pytest.mark.parametrize("width,ffn", [(128, 384), (256, 512)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rms_mode_through_the_c_abi(gpu_device, width, ffn, dtype):
+    """sah_mlp_residual_norm with SAH_NORM_RMS (called through ctypes; the
+    model wrapper passes SAH_NORM_LAYER): the residual equals the LayerNorm
+    mode's bit for bit (the FFN and the add do not depend on the norm), and
+    the normalized output equals sah_norm's RMSNorm of that residual bit for
+    bit, at widths 128 and 256; and it is within the 16-bit gate of float64
+    RMSNorm, x * rsqrt(mean(x^2) + eps) * gamma."""
+
+    from solution.kernels.boundary.hip_mlp_residual_norm import BLOCK_ROWS, NUM_WARPS, hip_mlp_residual_norm
+    from solution.kernels.hip._library import SAH_NORM_RMS, check_status, dtype_code, load_library, stream_handle
+    from solution.kernels.norm.hip_residual import hip_rms_norm
+
+    rows = 515
+    print(f"fused MLP RMS mode width {width} ffn {ffn} {dtype}", flush=True)
+    x, w1, b1, w2, b2, value = (t.to(gpu_device) for t in _operands(rows, width, ffn, dtype, seed=width + 7))
+    ln = _layer_norm(width, dtype, gpu_device, seed=9)
+    rms = torch.nn.RMSNorm(width, eps=1e-5).to(device=gpu_device, dtype=dtype)
+    with torch.no_grad():
+        rms.weight.copy_(ln.weight)
+    residual = torch.empty_like(value)
+    normalized = torch.empty_like(value)
+    with torch.inference_mode():
+        r_layer, _, _ = hip_mlp_residual_norm(x, w1, b1, w2, b2, value, ln)
+        status = load_library().sah_mlp_residual_norm(
+            x.data_ptr(), w1.data_ptr(), b1.data_ptr(), w2.data_ptr(), b2.data_ptr(), value.data_ptr(),
+            rms.weight.data_ptr(), None, residual.data_ptr(), normalized.data_ptr(),
+            rows, width, ffn, width, 1e-5, dtype_code(dtype), SAH_NORM_RMS, BLOCK_ROWS, NUM_WARPS,
+            stream_handle(gpu_device),
+        )
+        check_status(status, "sah_mlp_residual_norm (RMS)")
+        y_rms, _ = hip_rms_norm(residual, rms.weight, eps=1e-5, normalized_dtype=dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(residual, r_layer), f"residual: {int((residual != r_layer).sum())} elements differ"
+    assert torch.equal(normalized, y_rms), f"normalized: {int((normalized != y_rms).sum())} elements differ"
+    r64 = residual.double().cpu()
+    y64 = r64 * torch.rsqrt((r64 * r64).mean(-1, keepdim=True) + 1e-5) * rms.weight.double().cpu()
+    result = parity_gate(y64.float(), normalized.float().cpu(), dtype)
+    print(f"  RMS normalized vs float64: max_abs={result.max_abs_error:.3g} failed={result.failed_elements}",
+          flush=True)
+    assert result.passed
