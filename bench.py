@@ -27,7 +27,10 @@ to the B=32 two-layer forward, an extrapolation labelled as such.
 ``semantic_check`` compares, in the same run, one sequence of the timed
 weights through the HIP program with the product's portable program on the
 GPU (bf16 and fp32), as the reference does before timing its long-sequence
-shape.  ``resident_gpu`` times C2 and C4 with their registry programs under
+shape; ``semantic_check.fp32_io`` runs the same weights as an fp32 model
+through the mixed program (fp16 projections and HIP attention, HIP mixed
+norms) against the fp32 portable program under the official rule, the check
+the reference records for its deployed program (ratio 0.2816).  ``resident_gpu`` times C2 and C4 with their registry programs under
 the reference's formal protocol (20 warm-up calls, 3 x 100 timed calls).
 
 ``roofline.traffic`` is the attention kernel's HBM bytes per launch measured
@@ -618,7 +621,7 @@ def _median(values):
     return ordered[middle] if len(ordered) % 2 else 0.5 * (ordered[middle - 1] + ordered[middle])
 
 
-def cpu_long_sequence(threads: int, *, blocks_timed: int = 24, full_layer: bool = False) -> dict:
+def cpu_long_sequence(threads: int, *, blocks_timed: int = 96, full_layer: bool = False) -> dict:
     """The CPU oracle on one layer of one sequence at the real length
     S = 100000 (fp32, official op order, the reference portable path's
     query-blocked attention: every 128-row block scores all S keys, so every
@@ -690,6 +693,9 @@ def cpu_long_sequence(threads: int, *, blocks_timed: int = 24, full_layer: bool 
            f"mean {1e3 * sum(block_times) / len(block_times):.1f} ms per block")
     return {
         "layer_ms": round(1e3 * layer_s, 1),
+        "layer_is_measured": full_layer,
+        "attention_blocks_timed": len(chosen),
+        "attention_blocks": len(starts),
         "forward_ms": round(1e3 * forward_s, 1),
         "sample": (
             f"fp32 CPU oracle (official op order, query-blocked attention), one layer of one sequence at "
@@ -848,7 +854,7 @@ def semantic_check(model, x) -> dict:
 
     from autotune.accuracy import gate_ratio, summarize_errors, summary_no_less_accurate
     from solution.config import portable_streamed_config
-    from solution.shape14.defaults import hip_streamed_config
+    from solution.shape14.defaults import hip_deployed_shape14_config, hip_mixed_streamed_config, hip_streamed_config
     from solution.transformer import UserOptimizedTransformer
 
     device = x.device
@@ -869,6 +875,47 @@ def semantic_check(model, x) -> dict:
     candidate = run(hip_streamed_config(microbatch_size=1), torch.bfloat16)
     reference_path = run(portable_streamed_config(), torch.bfloat16)
     exact = run(portable_streamed_config(), torch.float32)
+    # fp32 I/O with fp16 internals: the reference's own check of its deployed
+    # long-sequence program (fp32 model, fp16 projections and attention)
+    # against the fp32 portable program, here with the HIP kernels: that
+    # program's shape (fp32 FFN output projection and norms), and the one with
+    # fp16 branches throughout (HIP mixed norms).
+    fp32_io = {}
+    for name, factory in (("deployed_shape14", hip_deployed_shape14_config), ("mixed", hip_mixed_streamed_config)):
+        output = run(factory(microbatch_size=1), torch.float32)
+        ratio = gate_ratio(output, exact, atol=0.002, rtol=0.02)
+        errors = summarize_errors(output, exact, atol=0.002, rtol=0.02)
+        fp32_io[name] = {"program": factory.__name__, "official_ratio_rtol0.02_atol0.002": round(ratio, 4),
+                         "official_passed": bool(ratio <= 1.0), "max_abs": round(errors.max_abs, 6),
+                         "mean_abs": round(errors.mean_abs, 7)}
+        del output
+    # The same check on the reference's own Shape 14 (F=1024, PyTorch default
+    # init, fp32 input): the configuration its recorded ratio was measured on.
+    w = WORKLOAD
+    shape14_config = _Config(1, w["seq_len"], w["d_model"], w["heads"], 1024, w["layers"])
+    torch.manual_seed(1234)
+    shape14 = UserOptimizedTransformer(shape14_config)  # PyTorch default init
+    shape14_state = shape14.state_dict()
+    del shape14
+    generator = torch.Generator(device=device).manual_seed(1234)
+    shape14_x = torch.randn(1, w["seq_len"], w["d_model"], generator=generator, device=device)
+    outputs = []
+    for program in (hip_deployed_shape14_config(microbatch_size=1), portable_streamed_config()):
+        other = UserOptimizedTransformer(shape14_config)
+        other.load_state_dict(shape14_state)
+        other = other.to(device=device).eval()
+        other.configure_execution(config=program)
+        with torch.inference_mode():
+            outputs.append(other(shape14_x))
+        torch.cuda.synchronize()
+        del other
+    ratio = gate_ratio(outputs[0], outputs[1], atol=0.002, rtol=0.02)
+    errors = summarize_errors(outputs[0], outputs[1], atol=0.002, rtol=0.02)
+    fp32_io["reference_shape14"] = {
+        "program": "hip_deployed_shape14_config", "workload": "B1 S100000 D1024 H16 F1024 L2 fp32, default init",
+        "official_ratio_rtol0.02_atol0.002": round(ratio, 4), "official_passed": bool(ratio <= 1.0),
+        "max_abs": round(errors.max_abs, 6), "mean_abs": round(errors.mean_abs, 7)}
+    del outputs, shape14_x
     c, r = summarize_errors(candidate, exact), summarize_errors(reference_path, exact)
     strict = summarize_errors(candidate, reference_path)
     result = {
@@ -883,11 +930,24 @@ def semantic_check(model, x) -> dict:
         "gate_ratio_2e-2_1e-2": round(gate_ratio(candidate, reference_path, atol=2e-2, rtol=1e-2), 4),
         "official_ratio_rtol0.02_atol0.002": round(
             gate_ratio(candidate, reference_path, atol=0.002, rtol=0.02), 4),
+        "fp32_io": {
+            "what": "fp32 model with fp16 projections and the HIP fp16 attention, B=1 S=100000, against the "
+                    "fp32 portable program under the official rule: the timed weights under the reference's "
+                    "deployed program shape (hip_deployed_shape14_config: fp32 FFN output projection, HIP fp32 "
+                    "norms) and with fp16 branches throughout (hip_mixed_streamed_config: HIP mixed norms); and "
+                    "the reference's own Shape 14 (F=1024, default init) under hip_deployed_shape14_config",
+            **fp32_io,
+            "reference_ratio": 0.2816,
+            "reference_ratio_source": "the reference's Triton program, fp32 I/O with fp16 internals, F=1024, "
+                                      "default init, RTX 4080 (result/20260831T083857.848038Z/"
+                                      "final_performance.json:414)",
+        },
     }
     del candidate, reference_path, exact
     torch.cuda.empty_cache()
+    ratios = ", ".join(f"{name} {entry['official_ratio_rtol0.02_atol0.002']:.4f}" for name, entry in fp32_io.items())
     log(f"semantic check: passed={result['passed']} candidate max_abs {c.max_abs:.4g} vs reference path "
-        f"{r.max_abs:.4g} (against fp32)")
+        f"{r.max_abs:.4g} (against fp32); fp32 I/O official ratios {ratios}")
     return result
 
 
@@ -949,12 +1009,18 @@ def main() -> int:
             "cores": threads,
             "kind": "port",
             "sample": long_sequence["sample"],
-            "measured_layer_ms": long_sequence["layer_ms"],
+            # a layer of one sequence: measured in full with --cpu-full-layer,
+            # otherwise its attention scaled from the timed query blocks
+            ("measured_layer_ms" if long_sequence["layer_is_measured"] else "layer_ms_from_sampled_blocks"):
+                long_sequence["layer_ms"],
+            "attention_blocks_timed": long_sequence["attention_blocks_timed"],
+            "attention_blocks": long_sequence["attention_blocks"],
             "forward_is_extrapolated": True,
             "affinity_cpus": affinity,
             "cgroup_cpu_quota": quota,
         }
-        log(f"cpu baseline: layer {long_sequence['layer_ms'] / 1e3:.1f} s measured, forward "
+        log(f"cpu baseline: layer {long_sequence['layer_ms'] / 1e3:.1f} s "
+            f"({'measured' if long_sequence['layer_is_measured'] else 'attention from sampled blocks'}), forward "
             f"{baseline['value'] / 1e3:.0f} s extrapolated, {threads} threads")
         if not args.no_resident:
             cpu_other = cpu_configs(threads)

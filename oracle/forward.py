@@ -174,7 +174,7 @@ def dense_causal_attention(
 
     seq = q.shape[-2]
     scores = torch.matmul(q, k.transpose(-2, -1)) * scale
-    mask = torch.ones((seq, seq), dtype=torch.bool).triu(diagonal=1)
+    mask = torch.ones((seq, seq), dtype=torch.bool, device=q.device).triu(diagonal=1)
     scores = scores.masked_fill(mask, float("-inf"))
     probs = torch.softmax(scores.float(), dim=-1).to(q.dtype)
     return torch.matmul(probs, v)
@@ -208,10 +208,10 @@ def query_block_rows(
     softmax cast to the input dtype, then P V.  Every block does the same
     work, whatever its position (no key-side causal skipping)."""
 
-    key_positions = torch.arange(q.shape[-2])
+    key_positions = torch.arange(q.shape[-2], device=q.device)
     scores = torch.matmul(q[..., start:stop, :], k.transpose(-2, -1))
     scores.mul_(scale)
-    query_positions = torch.arange(start, stop)
+    query_positions = torch.arange(start, stop, device=q.device)
     scores.masked_fill_(key_positions[None, :] > query_positions[:, None], float("-inf"))
     probs = torch.softmax(scores.float(), dim=-1).to(q.dtype)
     return torch.matmul(probs, v)
