@@ -480,9 +480,12 @@ def config3_summary(repeat: int = 100, warmup: int = 2000, trials: int = 5) -> d
     }
 
 
-def kernel_alone(kind: str, repeat: int) -> int:
+def kernel_alone(kind: str, repeat: int, data: str = "random") -> int:
     """Run one kernel alone at the workload's per-chunk shape; print the
-    HIP-event duration of every launch."""
+    HIP-event duration of every launch.  ``data="constant"`` fills the
+    attention's packed QKV with one value instead of N(0,1) (same
+    instructions, far fewer switching bits: the chip's power-limited clock
+    then rises, which the clock counters of a profile show)."""
 
     import torch
 
@@ -500,6 +503,8 @@ def kernel_alone(kind: str, repeat: int) -> int:
         if kind == "attention":
             packed = torch.randn(batch, seq, 3 * width, generator=generator, device=device,
                                  dtype=torch.bfloat16)
+            if data == "constant":
+                packed.fill_(0.25)
             q, k, v = (t.transpose(1, 2) for t in packed.unflatten(-1, (3, heads, width // heads)).unbind(dim=2))
             scale = 1.0 / math.sqrt(width // heads)
             launch = HIP_LONG_SEQUENCE_ATTENTION_LAUNCH
@@ -969,6 +974,8 @@ def main() -> int:
                                              "boundary-ffn-torch", "attention-c3", "norm-c3"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
+    parser.add_argument("--data", choices=("random", "constant"), default="random",
+                        help="--kernel attention inputs: N(0,1) or one constant value (power/clock probe)")
     parser.add_argument("--resident", choices=tuple(RESIDENT_SHAPES),
                         help="time one resident configuration's forward alone (profiling)")
     args = parser.parse_args()
@@ -985,7 +992,7 @@ def main() -> int:
     if args.kernel in ("attention-c3", "norm-c3"):
         return config3_alone(args.kernel, max(1, args.repeat))
     if args.kernel is not None:
-        return kernel_alone(args.kernel, max(1, args.repeat))
+        return kernel_alone(args.kernel, max(1, args.repeat), args.data)
     if args.resident is not None:
         print(json.dumps(resident_latency(RESIDENT_SHAPES[args.resident])), flush=True)
         return 0
