@@ -322,18 +322,27 @@ def measured_traffic() -> float | None:
         return None
 
 
-def _config3_cases(kind: str, device, *, launches=None):
+def _config3_cases(kind: str, device, *, launches=None, abi: bool = False):
     """BASELINE configs[2], the operators alone: causal attention at B8 H16
     S2048 Dh64 (Q, K, V N(0,1)/sqrt(64), scale 1/8; V both [B, H, S, 64]
     contiguous, which the op stages to V^T, and seq-contiguous), or the fused
     residual + LayerNorm on [16384, 1024] bf16 N(0,1) over rotating buffers.
-    Returns (label, run, work) triples: FLOPs or bytes per launch."""
+    Returns (label, run, work) triples: FLOPs or bytes per launch.
+
+    ``abi``: each launch calls the C-ABI entry point (the drop-in boundary)
+    on preallocated outputs and workspace, so back-to-back launches measure
+    the device-side rate; otherwise the Python operator, which allocates its
+    outputs per call (at ~25 us per norm launch its host time can leave the
+    GPU idle between launches)."""
 
     import torch
 
+    from solution.kernels.hip._library import check_status, dtype_code, load_library, stream_handle
     from solution.kernels.norm import hip_residual
     from solution.shape14 import hip_streaming_dh64
 
+    library = load_library()
+    stream = stream_handle(device)
     generator = torch.Generator(device=device).manual_seed(1234)
     cases = []
     if kind == "attention-c3":
@@ -345,6 +354,8 @@ def _config3_cases(kind: str, device, *, launches=None):
         # the same V stored seq-contiguous ([B, H, 64, S] transposed view), as
         # the native QKV projection hands it over: no staging copy
         v_seq_major = v.transpose(-1, -2).contiguous().transpose(-1, -2)
+        output = torch.empty(8, 2048, 16 * 64, device=device, dtype=torch.bfloat16)
+        code = dtype_code(torch.bfloat16)
         if launches is None:
             launches = [
                 (block_m, warps, stages)
@@ -353,35 +364,59 @@ def _config3_cases(kind: str, device, *, launches=None):
                 for stages in (1, 2, 3)
                 if hip_streaming_dh64.launch_config_is_valid(block_m, 64, warps, stages)
             ]
+
+        def abi_launch(value, block_m, warps, stages, workspace):
+            status = library.sah_causal_attention_bsd(
+                q.data_ptr(), k.data_ptr(), value.data_ptr(), output.data_ptr(), 8, 16, 2048, 64,
+                *q.stride()[:3], *k.stride()[:3], *value.stride(), output.stride(0), output.stride(1),
+                0.125, code, block_m, 64, warps, stages,
+                None if workspace is None else workspace.data_ptr(),
+                0 if workspace is None else workspace.numel(), stream)
+            check_status(status, "sah_causal_attention_bsd")
+
         for block_m, warps, stages in launches:
             for layout, value in (("V bhsd", v), ("V seq-major", v_seq_major)):
-                cases.append((
-                    f"launch ({block_m}, 64, {warps}, {stages}) {layout}",
-                    lambda bm=block_m, w=warps, st=stages, value=value: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
-                        q, k, value, scale=0.125, block_m=bm, block_n=64, num_warps=w, num_stages=st),
-                    flops,
-                ))
+                if abi:
+                    need = library.sah_causal_attention_workspace_bytes(
+                        8, 16, 2048, 64, value.stride(2), value.stride(3), code)
+                    workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
+                    run = (lambda bm=block_m, w=warps, st=stages, value=value, ws=workspace:
+                           abi_launch(value, bm, w, st, ws))
+                else:
+                    run = (lambda bm=block_m, w=warps, st=stages, value=value:
+                           hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
+                               q, k, value, scale=0.125, block_m=bm, block_n=64, num_warps=w, num_stages=st))
+                cases.append((f"launch ({block_m}, 64, {warps}, {stages}) {layout}", run, flops))
     else:
-        # 6 input pairs and the outputs of the last 6 launches kept alive:
-        # every launch touches buffers last used ~0.8 GB earlier, more than
-        # twice the 256 MB Infinity Cache, so the rate is HBM's, not MALL's
+        # 6 input pairs and 6 output pairs: every launch touches buffers last
+        # used ~0.8 GB earlier, more than twice the 256 MB Infinity Cache, so
+        # the rate is HBM's, not MALL's
         sets = 6
         inputs = [
             (torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16),
              torch.randn(16384, 1024, generator=generator, device=device, dtype=torch.bfloat16))
             for _ in range(sets)
         ]
-        outputs = [None] * sets
+        outputs = [(torch.empty(16384, 1024, device=device, dtype=torch.bfloat16),
+                    torch.empty(16384, 1024, device=device, dtype=torch.bfloat16)) for _ in range(sets)]
         counter = [0]
         layer_norm = torch.nn.LayerNorm(1024).to(device=device, dtype=torch.bfloat16)
         nbytes = _norm_bytes(*inputs[0], layer_norm.weight, layer_norm.bias, 1e-5, torch.bfloat16)
+        code = dtype_code(torch.bfloat16)
 
         def rotating(block_rows, warps):
             index = counter[0] % sets
             counter[0] += 1
-            outputs[index] = None
-            outputs[index] = hip_residual.hip_residual_layer_norm(
-                *inputs[index], layer_norm, block_rows=block_rows, num_warps=warps)
+            (value, update), (residual, normalized) = inputs[index], outputs[index]
+            if abi:
+                status = library.sah_residual_norm(
+                    value.data_ptr(), update.data_ptr(), layer_norm.weight.data_ptr(), layer_norm.bias.data_ptr(),
+                    residual.data_ptr(), normalized.data_ptr(), 16384, 1024, 1e-5, code, code, code, code,
+                    0, block_rows, warps, stream)
+                check_status(status, "sah_residual_norm")
+            else:
+                hip_residual.hip_residual_layer_norm(
+                    value, update, layer_norm, block_rows=block_rows, num_warps=warps, out=normalized)
 
         for block_rows, warps in launches or ((2, 2), (4, 4), (8, 8), (16, 8)):
             cases.append((
@@ -416,8 +451,9 @@ def _back_to_back_ms(run, repeat: int, *, warmup: int = 1, trials: int = 1) -> f
 
 
 def config3_alone(kind: str, repeat: int) -> int:
-    """Time every implemented launch of one operator-alone case and print
-    each mean launch time and its rate."""
+    """Time every implemented launch of one operator-alone case through the
+    C ABI and through the Python operator; print each mean launch time and
+    its rate."""
 
     import torch
 
@@ -425,13 +461,17 @@ def config3_alone(kind: str, repeat: int) -> int:
 
     load_library()
     with torch.inference_mode():
-        for label, run, work in _config3_cases(kind, torch.device("cuda", 0)):
-            ms = _back_to_back_ms(run, repeat)
-            if kind == "attention-c3":
-                rate = f"{work / ms / 1e9:.1f} TFLOP/s ({100 * work / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)"
-            else:
-                rate = f"{work / ms / 1e6:.1f} GB/s ({100 * work / ms / 1e6 / PEAK_HBM_GBS:.1f}% of 8 TB/s)"
-            print(f"{kind} {label}: {ms:.4f} ms per launch (mean of {repeat} back-to-back), {rate}", flush=True)
+        device = torch.device("cuda", 0)
+        for abi in (True, False):
+            how = "C-ABI launches" if abi else "Python operator"
+            for label, run, work in _config3_cases(kind, device, abi=abi):
+                ms = _back_to_back_ms(run, repeat)
+                if kind == "attention-c3":
+                    rate = f"{work / ms / 1e9:.1f} TFLOP/s ({100 * work / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)"
+                else:
+                    rate = f"{work / ms / 1e6:.1f} GB/s ({100 * work / ms / 1e6 / PEAK_HBM_GBS:.1f}% of 8 TB/s)"
+                print(f"{kind} {label}: {ms:.4f} ms per launch (mean of {repeat} back-to-back, {how}), {rate}",
+                      flush=True)
     return 0
 
 
@@ -451,23 +491,32 @@ def config3_summary(repeat: int = 100, warmup: int = 2000, trials: int = 5) -> d
 
     device = torch.device("cuda", 0)
     with torch.inference_mode():
-        (_, run_bhsd, flops), (_, run_seq, _) = _config3_cases(
-            "attention-c3", device, launches=[(L.block_m, L.num_warps, L.num_stages)])
+        launch = [(L.block_m, L.num_warps, L.num_stages)]
+        norm_launch = [(DEFAULT_BLOCK_ROWS, DEFAULT_NUM_WARPS)]
+        (_, run_bhsd, flops), (_, run_seq, _) = _config3_cases("attention-c3", device, launches=launch, abi=True)
         attention_ms = _back_to_back_ms(run_bhsd, repeat, warmup=warmup, trials=trials)
         attention_seq_ms = _back_to_back_ms(run_seq, repeat, warmup=repeat, trials=trials)
-        del run_bhsd, run_seq
-        ((_, run_norm, nbytes),) = _config3_cases(
-            "norm-c3", device, launches=[(DEFAULT_BLOCK_ROWS, DEFAULT_NUM_WARPS)])
+        (_, run_op, _), _ = _config3_cases("attention-c3", device, launches=launch)
+        op_attention_ms = _back_to_back_ms(run_op, repeat, warmup=repeat, trials=trials)
+        del run_bhsd, run_seq, run_op
+        ((_, run_norm, nbytes),) = _config3_cases("norm-c3", device, launches=norm_launch, abi=True)
         norm_ms = _back_to_back_ms(run_norm, repeat, warmup=repeat, trials=trials)
+        ((_, run_norm_op, _),) = _config3_cases("norm-c3", device, launches=norm_launch)
+        op_norm_ms = _back_to_back_ms(run_norm_op, repeat, warmup=repeat, trials=trials)
     tflops = flops / attention_ms / 1e9
     tflops_seq = flops / attention_seq_ms / 1e9
     gbs = nbytes / norm_ms / 1e6
     log(f"config 3: attention {1e3 * attention_ms:.1f} us ({1e3 * attention_seq_ms:.1f} us seq-contiguous V), "
-        f"norm {1e3 * norm_ms:.1f} us")
+        f"norm {1e3 * norm_ms:.1f} us through the C ABI; Python operators {1e3 * op_attention_ms:.1f} us, "
+        f"{1e3 * op_norm_ms:.1f} us")
     return {
         "workload": "operators alone (BASELINE configs[2]): attention B8 H16 S2048 Dh64, norm [16384, 1024]",
-        "timing": f"median of {trials} means of {repeat} back-to-back launches, HIP events, "
-                  f"after {warmup} warm-up attention launches, before the forward",
+        "timing": f"median of {trials} means of {repeat} back-to-back C-ABI launches on preallocated outputs "
+                  f"(the drop-in boundary), HIP events, after {warmup} warm-up attention launches, before the "
+                  f"forward; python_operator_* the same launches through the Python operators, which allocate "
+                  f"their outputs per call",
+        "python_operator_attention_us": round(1e3 * op_attention_ms, 2),
+        "python_operator_norm_us": round(1e3 * op_norm_ms, 2),
         "attention_launch": [L.block_m, L.block_n, L.num_warps, L.num_stages],
         "attention_us": round(1e3 * attention_ms, 2),
         "attention_tflops": round(tflops, 1),
