@@ -450,7 +450,7 @@ def _back_to_back_ms(run, repeat: int, *, warmup: int = 1, trials: int = 1) -> f
     return sorted(means)[len(means) // 2]
 
 
-def config3_alone(kind: str, repeat: int) -> int:
+def config3_alone(kind: str, repeat: int, launches=None) -> int:
     """Time every implemented launch of one operator-alone case through the
     C ABI and through the Python operator; print each mean launch time and
     its rate."""
@@ -464,7 +464,7 @@ def config3_alone(kind: str, repeat: int) -> int:
         device = torch.device("cuda", 0)
         for abi in (True, False):
             how = "C-ABI launches" if abi else "Python operator"
-            for label, run, work in _config3_cases(kind, device, abi=abi):
+            for label, run, work in _config3_cases(kind, device, abi=abi, launches=launches):
                 ms = _back_to_back_ms(run, repeat)
                 if kind == "attention-c3":
                     rate = f"{work / ms / 1e9:.1f} TFLOP/s ({100 * work / ms / 1e9 / PEAK_BF16_TFLOPS:.1f}% of peak)"
@@ -1023,6 +1023,8 @@ def main() -> int:
                                              "boundary-ffn-torch", "attention-c3", "norm-c3"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
+    parser.add_argument("--launch", type=lambda text: tuple(int(x) for x in text.split(",")),
+                        help="--kernel attention-c3: one launch BLOCK_M,WARPS,STAGES; norm-c3: ROWS,WARPS")
     parser.add_argument("--data", choices=("random", "constant"), default="random",
                         help="--kernel attention inputs: N(0,1) or one constant value (power/clock probe)")
     parser.add_argument("--resident", choices=tuple(RESIDENT_SHAPES),
@@ -1039,7 +1041,7 @@ def main() -> int:
     if args.steps <= 0 or args.warmup < 0:
         raise SystemExit("--steps must be positive and --warmup non-negative")
     if args.kernel in ("attention-c3", "norm-c3"):
-        return config3_alone(args.kernel, max(1, args.repeat))
+        return config3_alone(args.kernel, max(1, args.repeat), None if args.launch is None else [args.launch])
     if args.kernel is not None:
         return kernel_alone(args.kernel, max(1, args.repeat), args.data)
     if args.resident is not None:
