@@ -843,16 +843,72 @@ def _percentile(values, q):
 RESIDENT_SHAPES = {"c2": (64, 256, 512, 8, 2048, 4), "c4": (16, 4096, 2048, 32, 8192, 2)}
 
 
-def resident_latency(shape: tuple, *, warmup: int = 20, repeats: int = 100, rounds: int = 3) -> dict:
+def _latency_rounds(model, x, *, warmup: int, repeats: int, rounds: int):
+    """The reference's latency protocol on one model: ``warmup`` calls, then
+    ``rounds`` rounds of ``repeats`` calls with HIP events around every call
+    and one synchronization per round.  Returns the per-call GPU intervals
+    (ms) and the host time each call took to return (ms, no synchronization:
+    the time the host spends submitting the forward's launches)."""
+
+    import time
+
+    import torch
+
+    samples, host = [], []
+    for _ in range(warmup):
+        model(x)
+    torch.cuda.synchronize()
+    for _ in range(rounds):
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+        for index in range(repeats):
+            starts[index].record()
+            t0 = time.perf_counter()
+            model(x)
+            host.append((time.perf_counter() - t0) * 1e3)
+            ends[index].record()
+        torch.cuda.synchronize()
+        samples.extend(a.elapsed_time(b) for a, b in zip(starts, ends))
+    return samples, host
+
+
+def _latency_summary(samples: list, repeats: int) -> dict:
+    median = _median(samples)
+    slow = [i for i, t in enumerate(samples) if t > 1.1 * median]
+    return {
+        "median_ms": round(median, 4),
+        "p90_ms": round(_percentile(samples, 0.9), 4),
+        "mean_ms": round(sum(samples) / len(samples), 4),
+        "min_ms": round(min(samples), 4),
+        "max_ms": round(max(samples), 4),
+        "calls_over_1.1x_median": len(slow),
+        "of_them_in_first_10_of_a_round": sum(1 for i in slow if i % repeats < 10),
+    }
+
+
+def resident_latency(shape: tuple, *, warmup: int = 20, repeats: int = 100, rounds: int = 3,
+                     graph: bool = False) -> dict:
     """GPU forward latency of a resident configuration under the reference's
     formal protocol (benchmarking/protocols.py:116-117: 20 warm-up calls,
     then 3 rounds of 100; official/torch_transformer_benchmark.py:477-506:
     events recorded around every call of a round, one synchronization per
     round), with the registry's program for the shape, bf16, seeded
-    Xavier-uniform weights and N(0,1) input."""
+    Xavier-uniform weights and N(0,1) input.
+
+    Beside the GPU intervals it reports the host time per call (how long
+    ``model(x)`` takes to return: the submission of the forward's launches)
+    and where the slow calls fall.  An interval reads above the kernels' own
+    time when the host submits more slowly than the GPU runs, so a host
+    close to the GPU's rate shows its jitter in the tail.  ``graph``: the
+    same protocol once more with the program's runtime set to HIP-graph
+    replay (one launch per forward), which takes the host out of the
+    interval."""
+
+    import dataclasses
 
     import torch
 
+    from solution.config import RuntimeBackend
     from solution.transformer import UserOptimizedTransformer
 
     batch, seq, width, heads, ffn, layers = shape
@@ -864,32 +920,32 @@ def resident_latency(shape: tuple, *, warmup: int = 20, repeats: int = 100, roun
     model.configure_execution(config=program)
     generator = torch.Generator(device=device).manual_seed(1234)
     x = torch.randn(batch, seq, width, generator=generator, device=device, dtype=torch.bfloat16)
-    samples = []
     with torch.inference_mode():
-        for _ in range(warmup):
-            model(x)
-        torch.cuda.synchronize()
-        for _ in range(rounds):
-            starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
-            ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
-            for index in range(repeats):
-                starts[index].record()
-                model(x)
-                ends[index].record()
-            torch.cuda.synchronize()
-            samples.extend(a.elapsed_time(b) for a, b in zip(starts, ends))
+        samples, host = _latency_rounds(model, x, warmup=warmup, repeats=repeats, rounds=rounds)
+        graph_summary = None
+        if graph and program.schedule.runtime is not RuntimeBackend.CUDA_GRAPH:
+            replayed = dataclasses.replace(
+                program, schedule=dataclasses.replace(program.schedule, runtime=RuntimeBackend.CUDA_GRAPH))
+            model.configure_execution(config=replayed)
+            graph_samples, graph_host = _latency_rounds(model, x, warmup=warmup, repeats=repeats, rounds=rounds)
+            graph_summary = {
+                "program": replayed.config_id,
+                **_latency_summary(graph_samples, repeats),
+                "host_median_ms": round(_median(graph_host), 4),
+            }
     del model, x
-    median = _median(samples)
-    return {
+    result = {
         "workload": f"B{batch} S{seq} D{width} H{heads} F{ffn} L{layers} bf16",
         "program": program.config_id,
-        "median_ms": round(median, 4),
-        "p90_ms": round(_percentile(samples, 0.9), 4),
-        "mean_ms": round(sum(samples) / len(samples), 4),
-        "min_ms": round(min(samples), 4),
+        **_latency_summary(samples, repeats),
+        "host_median_ms": round(_median(host), 4),
+        "host_p90_ms": round(_percentile(host, 0.9), 4),
         "samples": len(samples),
         "protocol": f"{warmup} warm-up calls, {rounds} rounds x {repeats} calls, HIP events per call",
     }
+    if graph_summary is not None:
+        result["graph_replay"] = graph_summary
+    return result
 
 
 def semantic_check(model, x) -> dict:
@@ -1054,7 +1110,7 @@ def main() -> int:
     gpu = gpu_benchmark(args.steps, args.warmup, check=not args.no_check)
     resident = None
     if not args.no_resident:
-        resident = {name: resident_latency(shape) for name, shape in RESIDENT_SHAPES.items()}
+        resident = {name: resident_latency(shape, graph=(name == "c2")) for name, shape in RESIDENT_SHAPES.items()}
         log(f"resident: C2 {resident['c2']['median_ms']} ms, C4 {resident['c4']['median_ms']} ms (median)")
     threads, affinity, quota = _cpu_cores()
     baseline = None

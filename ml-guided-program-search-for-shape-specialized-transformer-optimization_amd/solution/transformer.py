@@ -840,8 +840,11 @@ class UserOptimizedTransformer(nn.Module):
                 valid_token_mask.dtype,
                 tuple(valid_token_mask.shape),
             )
+        # The active config object itself (compared by identity first, by
+        # value otherwise): its config_id is a SHA-256 of its canonical JSON,
+        # too slow to form on every call.
         signature = (
-            self._active_config.config_id,
+            self._active_config,
             value.device,
             value.dtype,
             tuple(value.shape),
