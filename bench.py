@@ -13,8 +13,8 @@ Printed on stdout: ONE JSON line.  ``value`` is the forward latency in ms
 attention: achieved TFLOP/s = algorithmic FLOPs (4*B*H*Dh*S(S+1)/2 per
 launch) / the launches' mean duration, timed with HIP events recorded on the
 launch stream around every attention call inside the timed region (a call
-also runs the key-norm pre-pass and the V^T staging, about 0.6% of it, so the
-figure is slightly below the attention kernel's own).
+also runs the key-norm pre-pass, about 1% of it, so the figure is slightly
+below the attention kernel's own).
 ``cpu_baseline`` times the CPU oracle (fp32 official order, query-blocked
 attention, as the reference's portable path) on the box's host cores: one
 layer of one sequence at the real length S=100000, row-wise work in full and
@@ -325,7 +325,8 @@ def measured_traffic() -> float | None:
 def _config3_cases(kind: str, device, *, launches=None, abi: bool = False):
     """BASELINE configs[2], the operators alone: causal attention at B8 H16
     S2048 Dh64 (Q, K, V N(0,1)/sqrt(64), scale 1/8; V both [B, H, S, 64]
-    contiguous, which the op stages to V^T, and seq-contiguous), or the fused
+    contiguous, which the kernel reads as given, and seq-contiguous, which
+    the op first copies key-major into its workspace), or the fused
     residual + LayerNorm on [16384, 1024] bf16 N(0,1) over rotating buffers.
     Returns (label, run, work) triples: FLOPs or bytes per launch.
 
@@ -352,7 +353,7 @@ def _config3_cases(kind: str, device, *, launches=None, abi: bool = False):
         )
         flops = _attention_flops(q)
         # the same V stored seq-contiguous ([B, H, 64, S] transposed view), as
-        # the native QKV projection hands it over: no staging copy
+        # the native QKV projection's seq-major option hands it over
         v_seq_major = v.transpose(-1, -2).contiguous().transpose(-1, -2)
         output = torch.empty(8, 2048, 16 * 64, device=device, dtype=torch.bfloat16)
         code = dtype_code(torch.bfloat16)

@@ -18,8 +18,8 @@ build:
   GELU, the fused HIP Linear + exact-GELU kernel, or the whole FFN fused
   through its residual LayerNorm, where the plan builder accepts them), then
   the QKV path (hipBLASLt packed projection with zero-copy
-  views, the HIP projection writing head-major Q / K and the attention's
-  V^T layout, or that projection with the initial LayerNorm fused in), then
+  views, the HIP projection writing head-major Q / K / V, or that
+  projection with the initial LayerNorm fused in), then
   the residual boundary (hipBLASLt output projections
   followed by the HIP residual norm, or the fused HIP Linear + residual +
   LayerNorm boundary where the plan builder accepts it), then runtime, each

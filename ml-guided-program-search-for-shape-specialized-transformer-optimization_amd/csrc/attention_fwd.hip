@@ -8,7 +8,7 @@
 //
 // MI355X formulation (not a translation of the Triton program):
 //  * Each wavefront owns 32*QG query rows; a workgroup is 4 or 8 waves
-//    sharing K and V^T tiles of 64 keys staged in LDS (double buffered).
+//    sharing K and V tiles of 64 keys staged in LDS (double buffered).
 //  * The score tile is computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_{bf16,f16}: the B operand (Q^T) stays in registers for
 //    the whole kernel and every lane's accumulator column is ONE query row, so
@@ -20,10 +20,13 @@
 //    which is exactly the k-slice the next MFMA needs, so P^T goes from the
 //    score accumulator to the B operand of O^T = V^T P^T without any lane
 //    exchange (one packed fp32->16-bit conversion per pair).
-//  * V^T tiles come from a seq-contiguous V^T buffer (the caller's, or one
-//    written by transpose_v_kernel / long_prepare_kernel below), so every LDS
-//    read is a 16-byte ds_read_b128.  On the scaled-key path the 8-wave
-//    launch stages K and V^T by direct-to-LDS loads into a three-tile ring.
+//  * V is read key-major as the caller hands it over ([B, H, S, 64], any key
+//    stride, e.g. the packed QKV view) and staged in LDS like K; the PV
+//    A operand (V^T rows) comes out of LDS through ds_read_b64_tr_b16, the
+//    gfx950 transposed read, so no V^T copy is made.  A caller's
+//    seq-contiguous V^T is copied key-major first (transpose_vt_kernel).
+//    On the scaled-key path the 8-wave launch stages K and V by
+//    direct-to-LDS loads into a three-tile ring.
 //  * The kernel template is in attention_kernel.hpp; this file instantiates
 //    the plain path and holds the host code, attention_scaled.hip the
 //    scaled-key path.
@@ -34,7 +37,7 @@
 //    is invariant to the shift; only where P is rounded differs.
 //  * Grid: one workgroup per (batch*head, query tile).  The hardware deals
 //    workgroup ids round-robin over the 8 XCDs; ids are remapped so that all
-//    tiles of a head land on one XCD (its L2 keeps the head's K and V^T) and
+//    tiles of a head land on one XCD (its L2 keeps the head's K and V) and
 //    each XCD issues its heads in groups: within a group, longest (last)
 //    query tiles first across the group's heads.  The host sizes the groups
 //    to about two rounds of resident workgroups (see head_group_for), which
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   constexpr int BM = kWaves * 32 * QG;
 
   __shared__ __attribute__((aligned(16))) T k_lds[2][kBlockN][kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[2][kHeadDim][kVRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[2][kBlockN][kVKRow];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
 
   const T* qbase = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
-  const T* vbase = static_cast<const T*>(p.vt) + b * p.v_sb + h * p.v_sh;
+  const T* vbase = static_cast<const T*>(p.v) + b * p.v_sb + h * p.v_sh;
   T* obase = static_cast<T*>(p.o) + b * p.o_sb + (int64_t)h * kHeadDim;
 
   const int q0 = q_tile * BM;
@@ -132,7 +135,8 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
     }
   }
 
-  // ---- cooperative loads: 2 x 16 B of a K tile / a V^T tile per thread.
+  // ---- cooperative loads: 2 x 16 B of a K tile / a V tile per thread (both
+  // key-major).
   u32x4 k_pref[2], v_pref[2];
   auto load_k = [&](int tile) {
     const int k0 = tile * kBlockN;
@@ -148,14 +152,14 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   };
   auto load_v = [&](int tile) {
     const int k0 = tile * kBlockN;
-    const bool full = k0 + kBlockN <= S;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int chunk = tid + kThreads * i;
-      const int row = chunk >> 3;
+      const int key = k0 + (chunk >> 3);
       const int c8 = (chunk & 7) * 8;
-      const T* src = vbase + (int64_t)row * p.v_sd + k0 + c8;
-      v_pref[i] = full ? load16(src) : load8_guarded<T>(src, (int64_t)k0 + c8, S);
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (key < S) raw = load16(vbase + (int64_t)key * p.v_ss + c8);
+      v_pref[i] = raw;
     }
   };
   auto store_k = [&](int tile) {
@@ -188,6 +192,10 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   }
   const float c = p.c;
   const int a_row = k_row_for(l32);
+  // Transposed V reads (see attn_fwd_kernel): key row 16 u + 8 half + 4 r +
+  // (lane / 4) % 4, head_dim column 32 d + 16 ((lane / 16) % 2) + 4 (lane % 4).
+  const int vtr_row = 8 * half + ((lane >> 2) & 3);
+  const int vtr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // S^T(j) = K(j) Q^T (raw scores) for every group; each K fragment feeds QG MFMAs.
   auto scores = [&](int j, f32x16 (*s)[2]) {
@@ -258,14 +266,16 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
     }
     return lsum;
   };
-  // O^T += V^T(j) P^T(j) for every group; each V^T fragment feeds QG MFMAs.
+  // O^T += V^T(j) P^T(j) for every group; each V^T fragment (read transposed
+  // from the key-major V tile) feeds QG MFMAs.
   auto pv = [&](int j, V8 (*pb)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
         const V8 va =
-            *reinterpret_cast<const V8*>(&v_lds[j & 1][32 * d + l32][16 * u + 8 * half]);
+            lds_read_tr16_pair<V8>(&v_lds[j & 1][16 * u + vtr_row][32 * d + vtr_col],
+                                   &v_lds[j & 1][16 * u + 4 + vtr_row][32 * d + vtr_col]);
 #pragma unroll
         for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(va, pb[g][u], acc[g][d]);
       }
@@ -543,23 +553,18 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(AttnF32Params p) {
 //    (kblock), and every key times c rounded to fp16 (kc, [batch*heads]
 //    [key_tiles * 64][64]; rows past the sequence are not written);
 //  * Q: the largest |q| of the block (qblock; 0 when zero_q: the queries of a
-//    zero scale, which the attention reads as zero);
-//  * V (vt non-null): V^T tiles [batch*heads][64][seq_pad], zero-filled for
-//    keys in [S, seq_pad).
+//    zero scale, which the attention reads as zero).
 // Wave w takes tiles 2w and 2w + 1 of the block for K and Q: eight lanes per
 // row with 16 bytes each, so reads and fp16 writes are contiguous runs; fp32
-// sums of squares.  The V^T tiles go through LDS with all 256 threads.
+// sums of squares.  V is not touched: the attention kernels read it as given.
 struct PrepParams {
   const void* k;
   const void* q;
-  const void* v;
   float* knorm;
   float* kblock;
   float* qblock;
   f16* kc;
-  void* vt;
-  int64_t k_sb, k_sh, k_ss, q_sb, q_sh, q_ss, v_sb, v_sh, v_ss;
-  int64_t seq_pad;
+  int64_t k_sb, k_sh, k_ss, q_sb, q_sh, q_ss;
   float c;
   int zero_q;
   int heads, seq_len, key_tiles, num_row_blocks;
@@ -602,7 +607,6 @@ __device__ __forceinline__ float tile_max_sq(const T* base, int64_t ss, int tile
 template <typename T>
 __global__ __launch_bounds__(256) void long_prepare_kernel(PrepParams pp) {
   __shared__ float red[2][4];
-  __shared__ T tile[64][kHeadDim + 2];
   const int blk = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / pp.heads;
@@ -641,77 +645,46 @@ __global__ __launch_bounds__(256) void long_prepare_kernel(PrepParams pp) {
     pp.qblock[(int64_t)bh * pp.num_row_blocks + blk] = pp.zero_q ? 0.0f : sqrtf(q4);
   }
 
-  if (pp.vt == nullptr) return;  // uniform
-  typedef typename Vec8<T>::type V8;
-  const T* vbase = static_cast<const T*>(pp.v) + b * pp.v_sb + h * pp.v_sh;
-  T* dst = static_cast<T*>(pp.vt) + (int64_t)bh * kHeadDim * pp.seq_pad;
-  for (int t = t0; t < t_end; ++t) {
-    const int k0 = t * 64;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int chunk = tid + 256 * i;
-      const int row = chunk >> 3;
-      const int c8 = (chunk & 7) * 8;
-      const int key = k0 + row;
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (key < pp.seq_len) raw = load16(vbase + (int64_t)key * pp.v_ss + c8);
-      const V8 vals = __builtin_bit_cast(V8, raw);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tile[row][c8 + e] = vals[e];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int chunk = tid + 256 * i;
-      const int d = chunk >> 3;
-      const int c8 = (chunk & 7) * 8;
-      V8 vals;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vals[e] = tile[c8 + e][d];
-      store16(dst + (int64_t)d * pp.seq_pad + k0 + c8, __builtin_bit_cast(u32x4, vals));
-    }
-    __syncthreads();  // the tile is rewritten for the next 64 keys
-  }
 }
 
-// [B, H, S, 64] (head_dim contiguous, any seq stride) -> V^T [B, H, 64, S_pad]
-// contiguous, zero-filled for keys in [S, S_pad).  One workgroup per 64 keys.
+// A seq-contiguous V^T [B, H, 64, >=S] (seq stride 1, head_dim stride
+// vt_sd) -> V [B, H, S, 64] contiguous, the key-major layout the attention
+// kernels read.  One workgroup per 64 keys; keys at or past S are neither
+// read nor written.
 template <typename T>
-__global__ __launch_bounds__(256) void transpose_v_kernel(
-    const T* __restrict__ v, T* __restrict__ vt, int64_t v_sb, int64_t v_sh,
-    int64_t v_ss, int heads, int seq_len, int64_t seq_pad) {
-  __shared__ T tile[64][kHeadDim + 2];
+__global__ __launch_bounds__(256) void transpose_vt_kernel(
+    const T* __restrict__ vt, T* __restrict__ v, int64_t vt_sb, int64_t vt_sh,
+    int64_t vt_sd, int heads, int seq_len) {
+  typedef typename Vec8<T>::type V8;
+  __shared__ T tile[kHeadDim][64 + 2];  // [head_dim][key]
   const int bh = blockIdx.y;
   const int b = bh / heads;
   const int h = bh - b * heads;
   const int k0 = blockIdx.x * 64;
-  const T* src = v + b * v_sb + h * v_sh;
-  T* dst = vt + (int64_t)bh * kHeadDim * seq_pad;
+  const T* src = vt + b * vt_sb + h * vt_sh;
+  T* dst = v + (int64_t)bh * seq_len * kHeadDim;
   const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int chunk = tid + 256 * i;
-    const int row = chunk >> 3;
-    const int c8 = (chunk & 7) * 8;
-    const int key = k0 + row;
-    u32x4 raw = {0u, 0u, 0u, 0u};
-    if (key < seq_len) raw = load16(src + (int64_t)key * v_ss + c8);
-    typedef typename Vec8<T>::type V8;
-    const V8 vals = __builtin_bit_cast(V8, raw);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) tile[row][c8 + e] = vals[e];
-  }
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int chunk = tid + 256 * i;
     const int d = chunk >> 3;
     const int c8 = (chunk & 7) * 8;
-    typedef typename Vec8<T>::type V8;
+    const V8 vals = __builtin_bit_cast(
+        V8, load8_guarded<T>(src + (int64_t)d * vt_sd + k0 + c8, (int64_t)k0 + c8, seq_len));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[d][c8 + e] = vals[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int chunk = tid + 256 * i;
+    const int row = chunk >> 3;
+    const int c8 = (chunk & 7) * 8;
+    if (k0 + row >= seq_len) continue;
     V8 vals;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vals[e] = tile[c8 + e][d];
-    store16(dst + (int64_t)d * seq_pad + k0 + c8, __builtin_bit_cast(u32x4, vals));
+    for (int e = 0; e < 8; ++e) vals[e] = tile[c8 + e][row];
+    store16(dst + (int64_t)(k0 + row) * kHeadDim + c8, __builtin_bit_cast(u32x4, vals));
   }
 }
 
@@ -771,7 +744,7 @@ int resident_per_cu(const void* kernel, int threads) {
 // Heads per issue group (see tile_of).  Each XCD holds slots = CUs/8 x
 // resident workgroups at once; groups of about 2 x slots workgroups let the
 // longest tiles of a group start first while the group stays small enough to
-// keep its heads' K and V^T in the XCD's L2.  Measured on MI355X (bf16):
+// keep its heads' K and V in the XCD's L2.  Measured on MI355X (bf16):
 // B8 H16 S2048 0.150 -> 0.110 ms (256/64/8/2), B16 H32 S4096 1.74 -> 1.53 ms,
 // B4 H16 S8192 0.82 -> 0.69 ms; long sequences (hundreds of tiles per head)
 // get one head per group, the plain head-major order.  The CU count of the
@@ -828,15 +801,14 @@ int launch_attention(AttnParams prm, int block_m, int num_warps, int num_stages,
 }
 
 template <typename T>
-int launch_transpose(const void* v, void* vt, int64_t batch, int64_t heads,
-                     int64_t seq_len, int64_t v_sb, int64_t v_sh, int64_t v_ss,
-                     hipStream_t stream) {
-  const int64_t seq_pad = padded_seq(seq_len);
-  const dim3 grid((unsigned)(seq_pad / 64), (unsigned)(batch * heads)), block(256);
-  hipLaunchKernelGGL((transpose_v_kernel<T>), grid, block, 0, stream,
-                     static_cast<const T*>(v), static_cast<T*>(vt), v_sb, v_sh, v_ss,
-                     (int)heads, (int)seq_len, seq_pad);
-  return check_hip(hipGetLastError(), "V transpose launch");
+int launch_transpose_vt(const void* vt, void* v, int64_t batch, int64_t heads,
+                        int64_t seq_len, int64_t vt_sb, int64_t vt_sh, int64_t vt_sd,
+                        hipStream_t stream) {
+  const dim3 grid((unsigned)ceil_div(seq_len, 64), (unsigned)(batch * heads)), block(256);
+  hipLaunchKernelGGL((transpose_vt_kernel<T>), grid, block, 0, stream,
+                     static_cast<const T*>(vt), static_cast<T*>(v), vt_sb, vt_sh, vt_sd,
+                     (int)heads, (int)seq_len);
+  return check_hip(hipGetLastError(), "V^T transpose launch");
 }
 
 template <typename T>
@@ -868,11 +840,12 @@ size_t scaled_key_bytes(int64_t batch, int64_t heads, int64_t seq_len) {
 }
 
 // The regions of one call's workspace, in order: the three norm tables and
-// the fp16 scaled keys when the call runs the preparation launch, then V^T
-// when V is head_dim-contiguous.
+// the fp16 scaled keys when the call runs the preparation launch, then a
+// key-major copy of V when the caller hands over a seq-contiguous V^T (the
+// kernels read a head_dim-contiguous V as given).
 struct WorkspaceLayout {
-  size_t norm = 0, block = 0, kc = 0, vt = 0;
-  size_t total() const { return norm + block + kc + vt; }
+  size_t norm = 0, block = 0, kc = 0, vcopy = 0;
+  size_t total() const { return norm + block + kc + vcopy; }
 };
 
 // `prepared`: the call runs the preparation launch (long sequences on the
@@ -887,8 +860,8 @@ WorkspaceLayout workspace_layout(int64_t batch, int64_t heads, int64_t seq_len,
     layout.block = row_block_bytes(batch, heads, seq_len);
     layout.kc = scaled_key_bytes(batch, heads, seq_len);
   }
-  if (v_stride_d == 1)
-    layout.vt = (size_t)batch * (size_t)heads * (size_t)kHeadDim * (size_t)padded_seq(seq_len) * 2;
+  if (v_stride_d != 1)
+    layout.vcopy = (size_t)batch * (size_t)heads * (size_t)seq_len * (size_t)kHeadDim * 2;
   return layout;
 }
 
@@ -924,8 +897,9 @@ extern "C" size_t sah_causal_attention_workspace_bytes(int64_t batch, int64_t he
                                                        int64_t v_stride_d, int dtype) {
   (void)head_dim;
   (void)v_stride_s;
-  // The largest need over the launches: the pipelined launch (num_stages 3)
-  // needs only the V^T region.  The fp32 kernel reads K and V as given.
+  // The largest need over the launches (the plain launches; the pipelined
+  // launch, num_stages 3, needs at most the V copy).  The fp32 kernel reads K
+  // and V as given.
   return workspace_layout(batch, heads, seq_len, v_stride_d, dtype,
                           prepares(seq_len, 2, dtype)).total();
 }
@@ -1063,7 +1037,7 @@ int run_attention(
 
   // Workspace: the per-tile key-norm table, the per-block key and query norm
   // tables and the fp16 scaled keys (long sequences on the plain kernel),
-  // then (reference V layout only) V^T.
+  // then, for a seq-contiguous V^T, its key-major copy.
   const bool prepared = allow_prepare && prepares(seq_len, num_stages, dtype);
   const WorkspaceLayout layout =
       workspace_layout(batch, heads, seq_len, v_stride_d, dtype, prepared);
@@ -1077,8 +1051,7 @@ int run_attention(
   const size_t block_bytes = layout.block;
   const size_t kc_bytes = layout.kc;
   unsigned char* base = static_cast<unsigned char*>(workspace);
-  void* vt_space = layout.vt > 0 ? base + norm_bytes + block_bytes + kc_bytes : nullptr;
-  const int64_t seq_pad = padded_seq(seq_len);
+  void* vcopy_space = layout.vcopy > 0 ? base + norm_bytes + block_bytes + kc_bytes : nullptr;
   int status = SAH_OK;
   prm.knorm = nullptr;
   prm.kblock = nullptr;
@@ -1098,36 +1071,30 @@ int run_attention(
     return fail(SAH_ERR_INVALID_ARGUMENT,
                 "value needs a unit stride on the head_dim or the seq axis");
   }
-  // The tile loaders address 64 rows of K and of V^T at 32-bit byte offsets
-  // from a per-tile base: both row strides must be non-negative and 64 rows
-  // must span less than 2^31 bytes.
-  const int64_t vt_row_stride = (v_stride_d == 1) ? seq_pad : v_stride_d;
-  if (k_stride_s < 0 || vt_row_stride < 0 || k_stride_s >= ((int64_t)1 << 24) ||
-      vt_row_stride >= ((int64_t)1 << 24))
+  // The tile loaders address 64 key rows of K and of V at 32-bit byte
+  // offsets from a per-tile base: both row strides must be non-negative and
+  // 64 rows must span less than 2^31 bytes.
+  const int64_t v_row_stride = (v_stride_d == 1) ? v_stride_s : kHeadDim;
+  if (k_stride_s < 0 || v_row_stride < 0 || k_stride_s >= ((int64_t)1 << 24) ||
+      v_row_stride >= ((int64_t)1 << 24))
     return fail(SAH_ERR_UNSUPPORTED,
                 "key/value row strides must lie in [0, 2^24) elements (32-bit tile offsets)");
   // Long sequences (the plain kernel): one preparation launch writes the
-  // norm tables, the fp16 scaled keys and, for a head_dim-contiguous V, V^T.
+  // norm tables and the fp16 scaled keys.
   if (prepared) {
     PrepParams pp;
     pp.k = key;
     pp.q = query;
-    pp.v = value;
     pp.knorm = reinterpret_cast<float*>(base);
     pp.kblock = reinterpret_cast<float*>(base + norm_bytes);
     pp.qblock = pp.kblock + batch * heads * prm.num_row_blocks;
     pp.kc = reinterpret_cast<f16*>(base + norm_bytes + block_bytes);
-    pp.vt = v_stride_d == 1 ? vt_space : nullptr;
     pp.k_sb = k_stride_b;
     pp.k_sh = k_stride_h;
     pp.k_ss = k_stride_s;
     pp.q_sb = q_stride_b;
     pp.q_sh = q_stride_h;
     pp.q_ss = q_stride_s;
-    pp.v_sb = v_stride_b;
-    pp.v_sh = v_stride_h;
-    pp.v_ss = v_stride_s;
-    pp.seq_pad = seq_pad;
     pp.c = prm.c;
     pp.zero_q = prm.q_and == 0u ? 1 : 0;
     pp.heads = (int)heads;
@@ -1143,25 +1110,24 @@ int run_attention(
     prm.kc = pp.kc;
   }
   if (v_stride_d == 1) {
-    // Reference layout: V^T in the workspace (written by the preparation
-    // launch, or transposed here).
-    if (!prepared) {
-      status = (dtype == SAH_DTYPE_BF16)
-                   ? launch_transpose<bf16>(value, vt_space, batch, heads, seq_len,
-                                            v_stride_b, v_stride_h, v_stride_s, stream)
-                   : launch_transpose<f16>(value, vt_space, batch, heads, seq_len,
-                                           v_stride_b, v_stride_h, v_stride_s, stream);
-      if (status != SAH_OK) return status;
-    }
-    prm.vt = vt_space;
-    prm.v_sb = heads * kHeadDim * seq_pad;
-    prm.v_sh = kHeadDim * seq_pad;
-    prm.v_sd = seq_pad;
-  } else {
-    prm.vt = value;
+    // The reference layout (head_dim-contiguous, any key stride): read as
+    // given, transposed on the way from LDS into the PV operand.
+    prm.v = value;
     prm.v_sb = v_stride_b;
     prm.v_sh = v_stride_h;
-    prm.v_sd = v_stride_d;
+    prm.v_ss = v_stride_s;
+  } else {
+    // A seq-contiguous V^T: copied key-major into the workspace first.
+    status = (dtype == SAH_DTYPE_BF16)
+                 ? launch_transpose_vt<bf16>(value, vcopy_space, batch, heads, seq_len,
+                                             v_stride_b, v_stride_h, v_stride_d, stream)
+                 : launch_transpose_vt<f16>(value, vcopy_space, batch, heads, seq_len,
+                                            v_stride_b, v_stride_h, v_stride_d, stream);
+    if (status != SAH_OK) return status;
+    prm.v = vcopy_space;
+    prm.v_sb = heads * seq_len * kHeadDim;
+    prm.v_sh = seq_len * kHeadDim;
+    prm.v_ss = kHeadDim;
   }
   return (dtype == SAH_DTYPE_BF16)
              ? launch_attention<bf16>(prm, block_m, num_warps, num_stages, stream)
@@ -1174,7 +1140,8 @@ int run_attention(
 // ---------------------------------------------------------------------------
 // Variant of sah_causal_attention_bsd for callers that cannot allocate
 // device memory (code under HIP graph capture, tight serving loops): the
-// workspace (norm tables, fp16 scaled keys, V^T staging) lives in this
+// workspace (norm tables, fp16 scaled keys, the key-major copy of a
+// seq-contiguous V^T) lives in this
 // file-scope device array, of which each GPU holds its own copy for the life
 // of the process.
 // Kernel arguments need its device address, which differs per GPU and is
@@ -1219,7 +1186,8 @@ extern "C" int sah_causal_attention_bsd_static_workspace(
     int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
     int block_m, int block_n, int num_warps, int num_stages, sah_stream_t stream) {
   // The prepared layout when it fits the array; otherwise the plain kernel's
-  // shifted path for every workgroup, which needs at most the V^T region.
+  // shifted path for every workgroup, which needs at most the key-major copy
+  // of a seq-contiguous V^T.
   constexpr size_t kLimit = (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES;
   const bool prepare = prepares(seq_len, num_stages, dtype) &&
                        workspace_layout(batch, heads, seq_len, v_stride_d, dtype, true).total() <= kLimit;

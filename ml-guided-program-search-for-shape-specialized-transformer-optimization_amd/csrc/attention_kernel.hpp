@@ -22,7 +22,10 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kPad = 8;                   // 16-byte row padding in LDS
 constexpr int kKRow = kHeadDim + kPad;    // K tile row (elements)
-constexpr int kVRow = kBlockN + kPad;     // V^T tile row (elements)
+// V tiles stay key-major in LDS (64 keys x 64 head_dim); rows padded to
+// 160 bytes so that the transposed reads of a 16-lane group (four key rows,
+// 32 bytes each) fall on distinct banks.
+constexpr int kVKRow = kHeadDim + 16;
 constexpr float kLog2e = 1.4426950408889634f;
 // The plain kernel raises a row's softmax shift only when a tile maximum
 // exceeds it by more than this many powers of two (probabilities then stay
@@ -83,11 +86,11 @@ constexpr int64_t kKeyNormMinSeq = 4096;
 struct AttnParams {
   const void* q;
   const void* k;
-  const void* vt;  // [B][H][64][>=S], seq stride 1
+  const void* v;  // [B][H][S][64], head_dim stride 1, key stride v_ss
   void* o;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
-  int64_t v_sb, v_sh, v_sd;
+  int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_ss;
   int seq_len;
   int heads;
@@ -205,6 +208,31 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
 __device__ __forceinline__ int ring_swizzle(int r) {
   return ((r >> 1) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
 }
+// Chunk swizzle of the V half of a ring stage: logical chunk c of key row r
+// sits in slot c ^ v_ring_swizzle(r).  A transposed read of a 16-lane group
+// covers four consecutive key rows and two adjacent chunks of each; the
+// swizzle puts those eight chunks in eight distinct slots (distinct banks).
+__device__ __forceinline__ int v_ring_swizzle(int r) { return 2 * (r & 3); }
+
+// ds_read_b64_tr_b16: lane l of each 16-lane group receives element l % 4 of
+// the 8 bytes addressed by lanes 4 e + l / 4 of its group, e = 0..3.  When
+// lane j of the group addresses key row kb + j / 4 at head_dim column
+// d0 + 4 (j % 4), lane l therefore receives V[kb .. kb + 3][d0 + l]: four
+// consecutive keys of one head_dim column, the transposed operand.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  auto q = (__attribute__((address_space(3))) v4s*)(const_cast<void*>(p));
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(q));
+}
+// The eight keys of a PV A-operand fragment: two transposed reads, four key
+// rows apart.
+template <typename V8>
+__device__ __forceinline__ V8 lds_read_tr16_pair(const void* lo, const void* hi) {
+  const u32x2 a = lds_read_tr16(lo);
+  const u32x2 b = lds_read_tr16(hi);
+  return __builtin_bit_cast(V8, u32x4{a[0], a[1], b[0], b[1]});
+}
+
 // One 16-byte direct-to-LDS load per lane: lane i's bytes from
 // base + offset land at LDS byte lds + 16 i (base and lds wave-uniform,
 // moved to scalar registers here).  Written as assembly so the compiler does
@@ -267,14 +295,14 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   constexpr int CPT = (kBlockN * 8) / NT;    // 16-byte chunks of a tile per thread
 
   // The scaled-key path of the 8-wave launches (32 or 64 rows per wave)
-  // stages K and V^T by direct-to-LDS loads into a ring of three tiles (two
+  // stages K and V by direct-to-LDS loads into a ring of three tiles (two
   // in flight while one is read); the other kernels use padded double
   // buffers filled through registers.
   constexpr bool kDma = PATH == kPathScaled && STAGES == 2 && WAVES == 8;
   constexpr int kRing = 3;
-  constexpr int kRingStage = 2 * kBlockN * kHeadDim * (int)sizeof(T);  // K then V^T, 16 KiB
+  constexpr int kRingStage = 2 * kBlockN * kHeadDim * (int)sizeof(T);  // K then V, 16 KiB
   __shared__ __attribute__((aligned(16))) T k_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[kDma ? 1 : STAGES][kDma ? 1 : kHeadDim][kDma ? 8 : kVRow];
+  __shared__ __attribute__((aligned(16))) T v_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kVKRow];
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kDma ? kRing * kRingStage : 16];
 
   const int tid = threadIdx.x;
@@ -294,7 +322,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 
   const T* qbase = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh;
   const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
-  const T* vbase = static_cast<const T*>(p.vt) + b * p.v_sb + h * p.v_sh;
+  const T* vbase = static_cast<const T*>(p.v) + b * p.v_sb + h * p.v_sh;
   T* obase = static_cast<T*>(p.o) + b * p.o_sb + (int64_t)h * kHeadDim;
 
   const int q0 = q_tile * BM;
@@ -365,10 +393,11 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 
   const int a_row = k_row_for(l32);
 
-  // ---- cooperative tile loader: CPT x 16 B of K and of V^T per thread.
-  // Full tiles are read as buffer loads: a tile base in scalar registers
-  // plus this thread's 32-bit byte offset inside the tile (the host keeps
-  // 64 rows of K and of V^T within 2^31 bytes).
+  // ---- cooperative tile loader: CPT x 16 B of K and of V per thread (both
+  // key-major: 64 key rows of 128 bytes).  Full tiles are read as buffer
+  // loads: a tile base in scalar registers plus this thread's 32-bit byte
+  // offset inside the tile (the host keeps 64 rows of K and of V within
+  // 2^31 bytes).
   uint32_t k_off[CPT], v_off[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
@@ -376,14 +405,14 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
     const int row = chunk >> 3;
     const int c8 = (chunk & 7) * 8;
     k_off[i] = (uint32_t)(((int64_t)row * kss + c8) * (int64_t)sizeof(T));
-    v_off[i] = (uint32_t)(((int64_t)row * p.v_sd + c8) * (int64_t)sizeof(T));
+    v_off[i] = (uint32_t)(((int64_t)row * p.v_ss + c8) * (int64_t)sizeof(T));
   }
   u32x4 k_pref[CPT], v_pref[CPT];
   auto load_tile = [&](int tile) {
     const int k0 = tile * kBlockN;
     if (k0 + kBlockN <= S) {  // tile-uniform: every key of the tile exists
       const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + (int64_t)k0 * kss);
-      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + k0);
+      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + (int64_t)k0 * p.v_ss);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
         k_pref[i] = buffer_load16(kr, k_off[i]);
@@ -391,28 +420,17 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       }
     } else {
       const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kb + (int64_t)k0 * kss);
-      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + k0);
+      const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vbase + (int64_t)k0 * p.v_ss);
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int chunk = tid + NT * i;
-        const int row = chunk >> 3;
-        const int c8 = (chunk & 7) * 8;
-        u32x4 raw = {0u, 0u, 0u, 0u};
-        if (k0 + row < S) raw = buffer_load16(kr, k_off[i]);
-        k_pref[i] = raw;
-        // V^T: row = head-dim index, 8 consecutive keys from k0 + c8.
-        const int valid = S - k0 - c8;
-        if (valid >= 8) {
-          v_pref[i] = buffer_load16(vr, v_off[i]);
-        } else {
-          uint32_t h[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            h[e] = (e < valid) ? (uint32_t)__builtin_bit_cast(
-                                     unsigned short, __builtin_amdgcn_raw_buffer_load_b16(vr, v_off[i] + 2 * e, 0, 0))
-                               : 0u;
-          v_pref[i] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        const int row = (tid + NT * i) >> 3;
+        u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
+        if (k0 + row < S) {  // rows past the sequence stay zero
+          kraw = buffer_load16(kr, k_off[i]);
+          vraw = buffer_load16(vr, v_off[i]);
         }
+        k_pref[i] = kraw;
+        v_pref[i] = vraw;
       }
     }
   };
@@ -429,11 +447,13 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
 
   // Ring loader (kDma): the 16 bytes of lane l of wave w land at tile row
   // dr = 8 w + l / 8, slot l % 8, so they carry logical chunk
-  // dc = (l % 8) ^ ring_swizzle(dr) of that row of K and of V^T.
+  // (l % 8) ^ ring_swizzle(dr) of key row dr of K and
+  // (l % 8) ^ v_ring_swizzle(dr) of key row dr of V.
   const int dr = wave * 8 + (lane >> 3);
   const int dc = (lane & 7) ^ ring_swizzle(dr);
+  const int dcv = (lane & 7) ^ v_ring_swizzle(dr);
   const uint32_t k_ring_off = (uint32_t)(((int64_t)dr * kss + 8 * dc) * (int64_t)sizeof(T));
-  const uint32_t v_ring_off = (uint32_t)(((int64_t)dr * p.v_sd + 8 * dc) * (int64_t)sizeof(T));
+  const uint32_t v_ring_off = (uint32_t)(((int64_t)dr * p.v_ss + 8 * dcv) * (int64_t)sizeof(T));
   const uint32_t ring_lds =
       (uint32_t)(uintptr_t)((__attribute__((address_space(3))) unsigned char*)ring);
   // Fills ring stage `stage` with tile `tile`; returns whether it issued
@@ -442,43 +462,40 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   auto fill_ring = [&](int tile, int stage) -> bool {
     const int k0 = tile * kBlockN;
     const T* kt = kb + (int64_t)k0 * kss;
-    const T* vt = vbase + k0;
+    const T* vt = vbase + (int64_t)k0 * p.v_ss;
     const uint32_t dst = ring_lds + stage * kRingStage + wave * 1024;
     if (k0 + kBlockN <= S) {
       dma16(kt, k_ring_off, dst);
       dma16(vt, v_ring_off, dst + kRingStage / 2);
       return true;
     }
-    const __amdgpu_buffer_rsrc_t kr = tile_rsrc(kt);
-    const __amdgpu_buffer_rsrc_t vr = tile_rsrc(vt);
     u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
-    if (k0 + dr < S) kraw = buffer_load16(kr, k_ring_off);
-    const int valid = S - k0 - 8 * dc;
-    if (valid >= 8) {
-      vraw = buffer_load16(vr, v_ring_off);
-    } else {
-      uint32_t h[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        h[e] = (e < valid) ? (uint32_t)__builtin_bit_cast(
-                                 unsigned short, __builtin_amdgcn_raw_buffer_load_b16(vr, v_ring_off + 2 * e, 0, 0))
-                           : 0u;
-      vraw = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    if (k0 + dr < S) {  // rows past the sequence stay zero
+      kraw = buffer_load16(tile_rsrc(kt), k_ring_off);
+      vraw = buffer_load16(tile_rsrc(vt), v_ring_off);
     }
     unsigned char* slot = ring + stage * kRingStage + wave * 1024 + lane * 16;
     *reinterpret_cast<u32x4*>(slot) = kraw;
     *reinterpret_cast<u32x4*>(slot + kRingStage / 2) = vraw;
     return false;
   };
-  // Operand fragments: K rows 32 t + a_row, chunk 2 s + half; V^T rows
-  // 32 d + l32, chunk 2 u + half.  In the ring, their byte offsets inside a
-  // stage are kept for the whole loop, so every operand read is one register
-  // plus an immediate (stage, subtile).
-  uint32_t k_ring_at[4], v_ring_at[4];
+  // Operand fragments.  K: rows 32 t + a_row, chunk 2 s + half (one 16-byte
+  // read).  V: the PV A operand (head_dim rows 32 d + l32, keys 16 u + 8 half
+  // .. + 7) from the key-major V tile by two transposed reads; lane l
+  // addresses key row 16 u + 8 half + 4 r + (l / 4) % 4 at head_dim column
+  // 32 d + 16 ((l / 16) % 2) + 4 (l % 4), r = 0, 1.  In the ring, the
+  // in-stage byte offsets are kept for the whole loop, so every operand read
+  // is one register plus an immediate (stage, subtile, r).
+  const int vtr_row = 8 * half + ((lane >> 2) & 3);
+  const int vtr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  uint32_t k_ring_at[4], v_ring_at[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 4; ++i)
     k_ring_at[i] = (uint32_t)(a_row * 128 + (((2 * i + half) ^ ring_swizzle(a_row)) << 4));
-    v_ring_at[i] = (uint32_t)(l32 * 128 + (((2 * i + half) ^ ring_swizzle(l32)) << 4));
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const int chunk = (2 * (32 * d + vtr_col)) >> 4;  // 16-byte chunk of the column
+    v_ring_at[d] = (uint32_t)(vtr_row * 128 + ((chunk ^ v_ring_swizzle(vtr_row)) << 4) + 8 * (lane & 1));
   }
   auto k_frag = [&](int stage, int t, int s) -> V8 {
     if constexpr (kDma)
@@ -487,11 +504,13 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       return *reinterpret_cast<const V8*>(&k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
   };
   auto v_frag = [&](int stage, int d, int u) -> V8 {
-    if constexpr (kDma)
-      return *reinterpret_cast<const V8*>(ring + stage * kRingStage + kRingStage / 2 + 32 * d * 128 +
-                                          v_ring_at[u]);
-    else
-      return *reinterpret_cast<const V8*>(&v_lds[stage][32 * d + l32][16 * u + 8 * half]);
+    if constexpr (kDma) {
+      const unsigned char* at = ring + stage * kRingStage + kRingStage / 2 + 16 * u * 128 + v_ring_at[d];
+      return lds_read_tr16_pair<V8>(at, at + 4 * 128);
+    } else {
+      const T* at = &v_lds[stage][16 * u + vtr_row][32 * d + vtr_col];
+      return lds_read_tr16_pair<V8>(at, at + 4 * kVKRow);
+    }
   };
 
   // ---- running state (lane-local: query l32 of each group).

@@ -28,8 +28,8 @@
 // bias added in fp32, one rounding, and every output column scattered
 // straight into query / key / value as [B, H, S, head_dim] (no [B, S, 3D]
 // intermediate).  The value may instead be written seq-contiguous,
-// [B, H, head_dim, v_ld], the layout the attention kernel reads its V^T
-// operand from, which saves the attention's own transpose pass.
+// [B, H, head_dim, v_ld], for consumers that want V^T (the attention kernel
+// reads the [B, H, S, head_dim] value as given).
 //
 // With a LayerNorm prologue (sah_norm_qkv_projection) the projection also
 // fuses the model's first LayerNorm, the reference's initial-norm / QKV fusion

@@ -664,7 +664,7 @@ HIP_DEFAULT_ATTENTION_LAUNCH = AttentionLaunchParams(
     block_m=128, block_n=64, num_warps=4, num_stages=2
 )
 # Long sequences: 256-row query tiles shared by 8 wavefronts, which halves the
-# K/V^T tile loads, LDS stores and barriers per FLOP against 128-row tiles
+# K/V tile loads, LDS stores and barriers per FLOP against 128-row tiles
 # (measured fastest of the 4/8-wave, 32/64-rows-per-wave launches on the
 # 100k-token chunk).  Short sequences keep 128-row tiles, which give twice as
 # many workgroups to fill 256 CUs.

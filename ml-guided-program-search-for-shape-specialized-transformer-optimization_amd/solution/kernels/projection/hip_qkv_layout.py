@@ -14,9 +14,9 @@ csrc/linear_gelu.hip).
 
 ``value_layout="seq_major"`` writes the value block seq-contiguous instead,
 into a [B, H, D/H, S8] buffer (S8 = S rounded up to 8) returned as its
-[B, H, S, D/H] view with strides (H*dh*S8, dh*S8, 1, S8): the operand layout
-the gfx950 attention kernel reads V^T from, so the attention needs no
-transpose pass and no workspace.
+[B, H, S, D/H] view with strides (H*dh*S8, dh*S8, 1, S8), for consumers
+that want V^T.  The gfx950 attention kernel reads the default [B, H, S, D/H]
+V as given (it copies a seq-contiguous V key-major first).
 
 Differences in domain from the reference (fp16, D in {32, 128, 1024},
 S in {32, 128, 1024}, H in {1, 2, 4, 16}): bf16 or fp16, any batch and

@@ -10,9 +10,10 @@ execution failed").  What differs is the implementation domain: bf16 or fp16
 inputs, any batch, head count and sequence length, head_dim 64, computed by
 the hand-written kernel in csrc/attention_fwd.hip.
 
-The value tensor may be the reference's head_dim-contiguous view (the kernel
-then writes V^T into a workspace first) or a seq-contiguous view of a V^T
-buffer, which the kernel reads directly.
+The value tensor may be the reference's head_dim-contiguous view (any key
+stride, e.g. the packed QKV view), which the kernel reads as given, or a
+seq-contiguous view of a V^T buffer, which it first copies key-major into
+its workspace.
 """
 
 from __future__ import annotations

@@ -319,8 +319,8 @@ class _SelfAttention(nn.Module):
             raise RuntimeError("the fused initial norm needs the HIP native-layout QKV projection")
         if plan.qkv_materialization is QKVMaterialization.HIP_NATIVE_BHSD:
             # The reference's native-layout branch (solution/transformer.py:384-431):
-            # the projection kernel writes head-major Q / K / V itself.  The HIP
-            # attention reads V^T, so V is written seq-contiguous for it.
+            # the projection kernel writes head-major Q / K / V itself, V as
+            # [B, H, S, 64], which the HIP attention reads as given.
             from .kernels.projection.hip_qkv_layout import (
                 HIP_INITIAL_NORM_QKV_BACKEND,
                 HIP_QKV_NATIVE_BHSD_BACKEND,
@@ -337,7 +337,7 @@ class _SelfAttention(nn.Module):
                 block_n=launch.block_n,
                 block_k=launch.block_k,
                 num_warps=launch.num_warps,
-                value_layout="seq_major" if backend is AttentionBackend.HIP_STREAMING_DH64 else "bhsd",
+                value_layout="bhsd",
             )
             if initial_norm is None:
                 query, key, projected, marker = prevalidated_hip_qkv_native_bhsd(

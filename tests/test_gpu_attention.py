@@ -152,10 +152,10 @@ def test_packed_qkv_view_and_transposed_value_layouts_agree(gpu_device):
 @pytest.mark.parametrize("block_m,num_warps", [(256, 8), (512, 8), (128, 4)])
 def test_long_sequence_value_layouts_agree_with_poisoned_padding(gpu_device, block_m, num_warps):
     """S = 16500 (scaled-key path; the last key tile is partial, and so is its
-    last 8-key chunk): V as the packed head_dim-contiguous view (staged into
-    the workspace's zero-padded V^T) and as a caller's seq-contiguous V^T
-    buffer whose columns past the sequence hold NaN give bitwise equal
-    outputs, so the staging never reads a key at or past S (a NaN times
+    last 8-key chunk): V as the packed head_dim-contiguous view (read as
+    given) and as a caller's seq-contiguous V^T buffer whose columns past the
+    sequence hold NaN (copied key-major into the workspace) give bitwise
+    equal outputs, so the copy never reads a key at or past S (a NaN times
     P = 0 would show)."""
 
     batch, seq, heads = 1, 16_500, 2
@@ -423,9 +423,9 @@ def test_scaled_key_path_near_its_bound_with_aligned_rows(gpu_device, dtype, bou
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("seq", [4095, 4096, 4097])
 def test_preparation_threshold_boundary(gpu_device, dtype, seq):
-    """4095 keys run the transpose and the shifted path, 4096 and more the
-    preparation launch and the scaled-key path (the workspace holds the norm
-    tables and scaled keys only then).  Every row on both sides of the
+    """4095 keys run the shifted path, 4096 and more the preparation launch
+    and the scaled-key path (with V in [B, H, S, 64] the workspace holds
+    only the norm tables and scaled keys, and only then).  Every row on both sides of the
     boundary against the fp32 oracle, under the 8-wave ring launch and a
     4-wave launch."""
 
@@ -433,9 +433,8 @@ def test_preparation_threshold_boundary(gpu_device, dtype, seq):
 
     library = _library.load_library()
     code = 1 if dtype == torch.float16 else 2
-    v_only = 2 * 64 * (-(-seq // 64) * 64) * 2
     workspace = library.sah_causal_attention_workspace_bytes(1, 2, seq, 64, 64, 1, code)
-    assert (workspace > v_only) == (seq >= 4096), (seq, workspace, v_only)
+    assert (workspace > 0) == (seq >= 4096), (seq, workspace)
     q, k, v = _inputs(1, 2, seq, dtype=dtype, seed=seq)
     reference = _to_bsd(_oracle(q, k, v, 1 / 8))
     for block_m, warps in ((256, 8), (128, 4)):
@@ -462,11 +461,8 @@ def test_scaled_keys_in_the_workspace(gpu_device):
     k[0, 1, 16_400] *= 5
     q[0, 2, 16_499] *= 7
     library = load_library()
-    vt = torch.zeros(batch, heads, 64, -(-seq // 64) * 64, dtype=torch.bfloat16)
-    vt[..., :seq] = v.transpose(-2, -1)
-    qd, kd, vtd = q.to(gpu_device), k.to(gpu_device), vt.to(gpu_device)
-    value = vtd[..., :seq].transpose(-2, -1)
-    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 1, value.stride(3), 2)
+    qd, kd, value = q.to(gpu_device), k.to(gpu_device), v.to(gpu_device)
+    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, value.stride(2), 1, 2)
     tiles = -(-seq // 64)
     row_blocks = -(-seq // 512)
     table = -(-(batch * heads * tiles * 4) // 256) * 256

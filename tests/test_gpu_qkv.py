@@ -128,9 +128,9 @@ def test_strided_rows_and_untouched_padding_through_the_c_abi(gpu_device):
 
 
 def test_seq_major_value_feeds_the_attention_bitwise(gpu_device):
-    """The attention reads the seq-contiguous value directly; with the
-    head_dim-contiguous value it first transposes it into its workspace.  Both
-    paths give the same V^T operand, so the outputs are bitwise equal."""
+    """The attention reads the head_dim-contiguous value as given; the
+    seq-contiguous value it first copies key-major into its workspace.  Both
+    paths give the same V operand, so the outputs are bitwise equal."""
 
     from solution.kernels.projection import hip_qkv_native_bhsd
     from solution.shape14.hip_streaming_dh64 import prevalidated_hip_streaming_dh64_causal_attention_bsd

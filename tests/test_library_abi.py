@@ -65,23 +65,26 @@ def test_host_only_entry_points():
     # (fp32, together rounded up to 256 bytes) ...
     blocks = -(-(2 * 2 * 16 * -(-100000 // 512) * 4) // 256) * 256
     assert blocks == 50176
-    # ... and every key times c in fp16, padded to 64 keys ...
+    # ... and every key times c in fp16, padded to 64 keys.  A head_dim-
+    # contiguous V (the reference layout, e.g. the packed QKV view) is read
+    # as given ...
     scaled_keys = 2 * 16 * 100032 * 64 * 2
-    # ... followed, when V is head_dim-contiguous, by V^T padded to 64 keys.
-    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 3072, 1, 2) == (
-        norms + blocks + scaled_keys + 2 * 16 * 64 * 100032 * 2
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 3072, 1, 2) == norms + blocks + scaled_keys
+    # ... and a seq-contiguous V^T adds its key-major copy (S x 64 per head).
+    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 1, 100032, 2) == (
+        norms + blocks + scaled_keys + 2 * 16 * 100000 * 64 * 2
     )
-    assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 1, 100032, 2) == norms + blocks + scaled_keys
     assert library.sah_causal_attention_workspace_bytes(1, 16, 16384, 64, 1, 16384, 1) == (
-        16 * 256 * 4 + 2 * 16 * 32 * 4 + 16 * 16384 * 128
+        16 * 256 * 4 + 2 * 16 * 32 * 4 + 16 * 16384 * 128 + 16 * 16384 * 128
     )
     # The tables and scaled keys start at 4096 keys.
-    assert library.sah_causal_attention_workspace_bytes(1, 2, 4096, 64, 1, 4096, 2) == 512 + 256 + 2 * 4096 * 128
-    assert library.sah_causal_attention_workspace_bytes(1, 2, 4095, 64, 1, 4096, 2) == 0
-    # Shorter sequences need only the V^T buffer, and seq-contiguous V none.
-    assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 64, 1, 2) == 8 * 16 * 64 * 2048 * 2
-    assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 1, 2048, 2) == 0
-    # fp32 reads K and V as given: no table, no V^T
+    assert library.sah_causal_attention_workspace_bytes(1, 2, 4096, 64, 64, 1, 2) == 512 + 256 + 2 * 4096 * 128
+    assert library.sah_causal_attention_workspace_bytes(1, 2, 4095, 64, 64, 1, 2) == 0
+    assert library.sah_causal_attention_workspace_bytes(1, 2, 4095, 64, 1, 4096, 2) == 2 * 4095 * 128
+    # Shorter sequences need nothing with V as given, the copy with V^T.
+    assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 64, 1, 2) == 0
+    assert library.sah_causal_attention_workspace_bytes(8, 16, 2048, 64, 1, 2048, 2) == 8 * 16 * 2048 * 64 * 2
+    # fp32 reads K and V as given: no table, no copy
     assert library.sah_causal_attention_workspace_bytes(2, 16, 100000, 64, 64, 1, 0) == 0
 
 
@@ -97,21 +100,17 @@ def test_invalid_arguments_fail_before_launch():
         fake, fake, fake, fake, 1, 1, 16, 32, *([0] * 12), 0.125, 2, 128, 64, 4, 2, None, 0, None
     )
     assert status == _library.SAH_ERR_UNSUPPORTED and b"head_dim" in library.sah_last_error()
-    # Tiles of 64 key rows are addressed at 32-bit offsets: key and V^T row
-    # strides outside [0, 2^24) elements are refused before any launch.
+    # Tiles of 64 key rows of K and of V are addressed at 32-bit offsets: key
+    # and value row strides outside [0, 2^24) elements are refused before any
+    # launch.
     def attend(seq, k_ss, v_ss, v_sd, workspace=None, workspace_bytes=0):
         return library.sah_causal_attention_bsd(
             fake, fake, fake, fake, 1, 1, seq, 64, 0, 0, 64, 0, 0, k_ss, 0, 0, v_ss, v_sd, 0, 64,
             0.125, 2, 128, 64, 4, 2, workspace, workspace_bytes, None)
 
-    for k_ss, v_sd in ((-64, 1024), (1 << 24, 1024), (64, 1 << 24), (64, -1024)):
-        assert attend(1000, k_ss, 1, v_sd) == _library.SAH_ERR_UNSUPPORTED, (k_ss, v_sd)
+    for k_ss, v_ss in ((-64, 64), (1 << 24, 64), (64, 1 << 24), (64, -64)):
+        assert attend(1000, k_ss, v_ss, 1) == _library.SAH_ERR_UNSUPPORTED, (k_ss, v_ss)
         assert b"32-bit tile offsets" in library.sah_last_error()
-    # the reference V layout stages V^T with rows of roundup(seq, 64) keys
-    long_seq = (1 << 24) + 1
-    need = library.sah_causal_attention_workspace_bytes(1, 1, long_seq, 64, 64, 1, 2)
-    assert attend(long_seq, 64, 64, 1, fake, need) == _library.SAH_ERR_UNSUPPORTED
-    assert b"32-bit tile offsets" in library.sah_last_error()
     status = library.sah_residual_norm(
         fake, fake, None, None, fake, fake, 4, 1000, 1e-5, 2, 2, 2, 0, 0, 4, 4, None
     )

@@ -1,10 +1,11 @@
 """sah_causal_attention_bsd_static_workspace, the attention entry point that
 allocates nothing (its workspace is a static device array), against
 sah_causal_attention_bsd with a caller-provided workspace.  Where the
-prepared long-sequence layout (norm tables, fp16 scaled keys, V^T) fits the
-array, both run the same kernels and the outputs must be bitwise equal.
-Where it does not, the static entry runs every workgroup on the plain
-kernel's shifted path (no preparation, at most the V^T region), and the
+prepared long-sequence layout (norm tables, fp16 scaled keys, and the
+key-major copy of a seq-contiguous V^T) fits the array, both run the same
+kernels and the outputs must be bitwise equal.  Where it does not, the
+static entry runs every workgroup on the plain kernel's shifted path (no
+preparation, at most the V copy), and the
 outputs must agree to the bf16/fp16 gate (|err| <= 2e-2 or |err| <= 1e-2
 |ref|).  Each case makes two calls in a row, the second on a smaller input,
 so the second reads the array the first left behind.  Both entry points are
@@ -65,12 +66,12 @@ CASES = [
 # the shifted path without preparation.  (dtype, seq-contiguous V, launch,
 # first, second smaller)
 FALLBACK_CASES = [
-    # BASELINE C4's attention (B16 H32 S4096) with V seq-contiguous: the
+    # BASELINE C4's attention (B16 H32 S4096) with V in [B, H, S, 64]: the
     # scaled keys alone are 268 MB; the shifted path needs no workspace.
-    (torch.bfloat16, True, (256, 64, 8, 2), (16, 32, 4096), (2, 16, 4500)),
-    # V in [B, H, S, 64]: tables + scaled keys + V^T just over 64 MiB, V^T
-    # alone (33.5 MB) fits.
-    (torch.bfloat16, False, (256, 64, 8, 2), (1, 16, 16384), (1, 8, 5000)),
+    (torch.bfloat16, False, (256, 64, 8, 2), (16, 32, 4096), (2, 16, 4500)),
+    # V seq-contiguous: tables + scaled keys + the key-major V copy just over
+    # 64 MiB, the copy alone (33.5 MB) fits.
+    (torch.bfloat16, True, (256, 64, 8, 2), (1, 16, 16384), (1, 8, 5000)),
 ]
 
 
@@ -134,15 +135,17 @@ def test_requests_beyond_the_static_workspace_are_rejected_before_launch(gpu_dev
     from solution.kernels.hip import _library
 
     library = load_library()
-    batch, heads, seq = 2, 16, 100000  # V^T alone is 410 MB
-    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 64, 1, 2)
+    # a seq-contiguous V^T: its key-major copy alone is 410 MB
+    batch, heads, seq = 2, 16, 100000
+    need = library.sah_causal_attention_workspace_bytes(batch, heads, seq, 64, 1, seq, 2)
     assert need > _library.ATTENTION_STATIC_WORKSPACE_BYTES
     # full-size buffers, so that no access could leave them even if a launch happened
     q = torch.zeros(batch, heads, seq, 64, dtype=torch.bfloat16, device=gpu_device)
+    value = torch.zeros(batch, heads, 64, seq, dtype=torch.bfloat16, device=gpu_device).transpose(-1, -2)
     out = torch.empty(batch, seq, heads * 64, dtype=torch.bfloat16, device=gpu_device)
     status = library.sah_causal_attention_bsd_static_workspace(
-        q.data_ptr(), q.data_ptr(), q.data_ptr(), out.data_ptr(), batch, heads, seq, 64,
-        *q.stride()[:3], *q.stride()[:3], *q.stride(), out.stride(0), out.stride(1),
+        q.data_ptr(), q.data_ptr(), value.data_ptr(), out.data_ptr(), batch, heads, seq, 64,
+        *q.stride()[:3], *q.stride()[:3], *value.stride(), out.stride(0), out.stride(1),
         0.125, 2, 256, 64, 8, 2, stream_handle(gpu_device))
     assert status == _library.SAH_ERR_WORKSPACE
     assert b"static workspace" in library.sah_last_error()
