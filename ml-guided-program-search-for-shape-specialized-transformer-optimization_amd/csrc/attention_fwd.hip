@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   constexpr int BM = kWaves * 32 * QG;
 
   __shared__ __attribute__((aligned(16))) T k_lds[2][kBlockN][kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[2][kBlockN][kVKRow];
+  __shared__ __attribute__((aligned(16))) unsigned char v_lds[2][kVTileBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int chunk = tid + kThreads * i;
-      *reinterpret_cast<u32x4*>(&v_lds[tile & 1][chunk >> 3][(chunk & 7) * 8]) = v_pref[i];
+      *reinterpret_cast<u32x4*>(&v_lds[tile & 1][v_store_offset(chunk >> 3, (chunk & 7) * 8)]) = v_pref[i];
     }
   };
 
@@ -192,10 +192,8 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
   }
   const float c = p.c;
   const int a_row = k_row_for(l32);
-  // Transposed V reads (see attn_fwd_kernel): key row 16 u + 8 half + 4 r +
-  // (lane / 4) % 4, head_dim column 32 d + 16 ((lane / 16) % 2) + 4 (lane % 4).
-  const int vtr_row = 8 * half + ((lane >> 2) & 3);
-  const int vtr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // Transposed V reads (see attn_fwd_kernel): in-tile byte offsets.
+  const uint32_t v_at[2] = {v_tr_offset(lane, 0), v_tr_offset(lane, 1)};
 
   // S^T(j) = K(j) Q^T (raw scores) for every group; each K fragment feeds QG MFMAs.
   auto scores = [&](int j, f32x16 (*s)[2]) {
@@ -274,8 +272,8 @@ __global__ __launch_bounds__(kThreads, QG == 1 ? 2 : 1) void attn_fwd_pipelined_
 #pragma unroll
       for (int d = 0; d < 2; ++d) {
         const V8 va =
-            lds_read_tr16_pair<V8>(&v_lds[j & 1][16 * u + vtr_row][32 * d + vtr_col],
-                                   &v_lds[j & 1][16 * u + 4 + vtr_row][32 * d + vtr_col]);
+            lds_read_tr16_pair<V8>(&v_lds[j & 1][16 * u * 128 + v_at[d]],
+                                   &v_lds[j & 1][16 * u * 128 + 512 + v_at[d]]);
 #pragma unroll
         for (int g = 0; g < QG; ++g) acc[g][d] = mfma32(va, pb[g][u], acc[g][d]);
       }

@@ -22,10 +22,10 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kPad = 8;                   // 16-byte row padding in LDS
 constexpr int kKRow = kHeadDim + kPad;    // K tile row (elements)
-// V tiles stay key-major in LDS (64 keys x 64 head_dim); rows padded to
-// 160 bytes so that the transposed reads of a 16-lane group (four key rows,
-// 32 bytes each) fall on distinct banks.
-constexpr int kVKRow = kHeadDim + 16;
+// V tiles stay key-major in LDS: 64 key rows of 128 bytes, each row's 16-byte
+// chunks permuted by v_ring_swizzle (below), in the direct-to-LDS ring and in
+// the register-staged buffers alike.
+constexpr int kVTileBytes = kBlockN * kHeadDim * 2;
 constexpr float kLog2e = 1.4426950408889634f;
 // The plain kernel raises a row's softmax shift only when a tile maximum
 // exceeds it by more than this many powers of two (probabilities then stay
@@ -208,11 +208,28 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint
 __device__ __forceinline__ int ring_swizzle(int r) {
   return ((r >> 1) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
 }
-// Chunk swizzle of the V half of a ring stage: logical chunk c of key row r
+// Chunk swizzle of a key-major V tile in LDS: logical chunk c of key row r
 // sits in slot c ^ v_ring_swizzle(r).  A transposed read of a 16-lane group
 // covers four consecutive key rows and two adjacent chunks of each; the
-// swizzle puts those eight chunks in eight distinct slots (distinct banks).
+// swizzle puts those eight chunks in eight distinct slots (distinct banks;
+// measured: no bank conflicts, where 160-byte padded rows without the
+// swizzle conflicted).
 __device__ __forceinline__ int v_ring_swizzle(int r) { return 2 * (r & 3); }
+// Byte offset, inside a V tile, of this lane's first transposed read of the
+// PV operand for head_dim block d (add 16 u * 128 for keys 16 u .., and 512
+// for the second read, four key rows further): key row
+// 8 (lane / 32) + (lane / 4) % 4, head_dim column 32 d + 16 ((lane / 16) % 2)
+// + 4 (lane % 4).
+__device__ __forceinline__ uint32_t v_tr_offset(int lane, int d) {
+  const int row = 8 * (lane >> 5) + ((lane >> 2) & 3);
+  const int col = 32 * d + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int chunk = (2 * col) >> 4;
+  return (uint32_t)(row * 128 + ((chunk ^ v_ring_swizzle(row)) << 4) + ((2 * col) & 15));
+}
+// Byte offset of chunk c8 / 8 of key row `row` in a V tile.
+__device__ __forceinline__ uint32_t v_store_offset(int row, int c8) {
+  return (uint32_t)(row * 128 + (((c8 >> 3) ^ v_ring_swizzle(row)) << 4));
+}
 
 // ds_read_b64_tr_b16: lane l of each 16-lane group receives element l % 4 of
 // the 8 bytes addressed by lanes 4 e + l / 4 of its group, e = 0..3.  When
@@ -302,7 +319,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   constexpr int kRing = 3;
   constexpr int kRingStage = 2 * kBlockN * kHeadDim * (int)sizeof(T);  // K then V, 16 KiB
   __shared__ __attribute__((aligned(16))) T k_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kKRow];
-  __shared__ __attribute__((aligned(16))) T v_lds[kDma ? 1 : STAGES][kDma ? 1 : kBlockN][kDma ? 8 : kVKRow];
+  __shared__ __attribute__((aligned(16))) unsigned char v_lds[kDma ? 1 : STAGES][kDma ? 16 : kVTileBytes];
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kDma ? kRing * kRingStage : 16];
 
   const int tid = threadIdx.x;
@@ -441,7 +458,7 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       const int row = chunk >> 3;
       const int c8 = (chunk & 7) * 8;
       *reinterpret_cast<u32x4*>(&k_lds[stage][row][c8]) = k_pref[i];
-      *reinterpret_cast<u32x4*>(&v_lds[stage][row][c8]) = v_pref[i];
+      *reinterpret_cast<u32x4*>(&v_lds[stage][v_store_offset(row, c8)]) = v_pref[i];
     }
   };
 
@@ -481,22 +498,15 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
   };
   // Operand fragments.  K: rows 32 t + a_row, chunk 2 s + half (one 16-byte
   // read).  V: the PV A operand (head_dim rows 32 d + l32, keys 16 u + 8 half
-  // .. + 7) from the key-major V tile by two transposed reads; lane l
-  // addresses key row 16 u + 8 half + 4 r + (l / 4) % 4 at head_dim column
-  // 32 d + 16 ((l / 16) % 2) + 4 (l % 4), r = 0, 1.  In the ring, the
-  // in-stage byte offsets are kept for the whole loop, so every operand read
-  // is one register plus an immediate (stage, subtile, r).
-  const int vtr_row = 8 * half + ((lane >> 2) & 3);
-  const int vtr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  uint32_t k_ring_at[4], v_ring_at[2];
+  // .. + 7) from the key-major V tile by two transposed reads (v_tr_offset).
+  // The in-tile byte offsets are kept for the whole loop, so every operand
+  // read is one register plus an immediate (stage, subtile, second read).
+  uint32_t k_ring_at[4], v_at[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     k_ring_at[i] = (uint32_t)(a_row * 128 + (((2 * i + half) ^ ring_swizzle(a_row)) << 4));
 #pragma unroll
-  for (int d = 0; d < 2; ++d) {
-    const int chunk = (2 * (32 * d + vtr_col)) >> 4;  // 16-byte chunk of the column
-    v_ring_at[d] = (uint32_t)(vtr_row * 128 + ((chunk ^ v_ring_swizzle(vtr_row)) << 4) + 8 * (lane & 1));
-  }
+  for (int d = 0; d < 2; ++d) v_at[d] = v_tr_offset(lane, d);
   auto k_frag = [&](int stage, int t, int s) -> V8 {
     if constexpr (kDma)
       return *reinterpret_cast<const V8*>(ring + stage * kRingStage + 32 * t * 128 + k_ring_at[s]);
@@ -504,13 +514,9 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       return *reinterpret_cast<const V8*>(&k_lds[stage][32 * t + a_row][16 * s + 8 * half]);
   };
   auto v_frag = [&](int stage, int d, int u) -> V8 {
-    if constexpr (kDma) {
-      const unsigned char* at = ring + stage * kRingStage + kRingStage / 2 + 16 * u * 128 + v_ring_at[d];
-      return lds_read_tr16_pair<V8>(at, at + 4 * 128);
-    } else {
-      const T* at = &v_lds[stage][16 * u + vtr_row][32 * d + vtr_col];
-      return lds_read_tr16_pair<V8>(at, at + 4 * kVKRow);
-    }
+    const unsigned char* tile = kDma ? ring + stage * kRingStage + kRingStage / 2 : &v_lds[stage][0];
+    const unsigned char* at = tile + 16 * u * 128 + v_at[d];
+    return lds_read_tr16_pair<V8>(at, at + 4 * 128);
   };
 
   // ---- running state (lane-local: query l32 of each group).
