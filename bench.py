@@ -478,8 +478,9 @@ def config3_alone(kind: str, repeat: int, launches=None) -> int:
 
 def config3_summary(repeat: int = 100, warmup: int = 2000, trials: int = 5) -> dict:
     """The operator-alone figures reported beside the forward: attention with
-    the long-sequence launch (V in the reference's [B, H, S, 64] layout, V^T
-    staging included, and seq-contiguous), the norm with its default launch.
+    the long-sequence launch (V in the reference's [B, H, S, 64] layout, read
+    as given, and a seq-contiguous V^T, its key-major copy included), the
+    norm with its default launch.
     Each figure is the median of `trials` means of `repeat` back-to-back
     launches.  The first case runs `warmup` untimed launches (about 0.2 s)
     that bring the idle chip to its clock: the first hundreds of launches

@@ -67,15 +67,16 @@ const char* sah_last_error(void);
  * dtype: SAH_DTYPE_BF16 or SAH_DTYPE_F16 for q, k, v and output.
  * q/k: the head_dim stride must be 1, the seq stride a multiple of 8 and the
  *      base 16-byte aligned; the key seq stride must lie in [0, 2^24).
- * v:   either head_dim-contiguous (v_stride_d == 1, the reference layout; the
- *      kernel then first writes V^T into `workspace`, so seq_len rounded up
- *      to 64 must stay below 2^24) or seq-contiguous (v_stride_s == 1, a V^T
- *      buffer whose v_stride_d must lie in [0, 2^24)).  Tiles of 64 key rows
- *      are addressed at 32-bit offsets; larger strides return
- *      SAH_ERR_UNSUPPORTED.
+ * v:   either head_dim-contiguous (v_stride_d == 1, the reference layout,
+ *      any key stride in [0, 2^24) such as the packed QKV view's; read as
+ *      given, the PV operand transposed on its way out of LDS) or
+ *      seq-contiguous (v_stride_s == 1, a V^T buffer, any v_stride_d that is
+ *      a multiple of 8; first copied key-major into `workspace`).  Tiles of
+ *      64 key rows are addressed at 32-bit offsets; a larger key stride
+ *      returns SAH_ERR_UNSUPPORTED.
  * workspace: 16-byte aligned, at least sah_causal_attention_workspace_bytes();
  *      may be null when that is 0.  Sequences of 4096 keys or more keep
- *      there, written by one preparation launch over Q, K (and V): a table
+ *      there, written by one preparation launch over Q and K: a table
  *      of the largest key norm of every 64-key tile, which bounds every score
  *      so that most tiles skip their row maximum, tables of the largest key
  *      and query norm of every 512-row block, and the keys times
@@ -106,9 +107,10 @@ int sah_causal_attention_bsd(
  * launches): for seq_len >= 4096 the key-norm table (4 bytes per 64-key tile
  * per head, rounded up to 256), the key and query block-norm tables (8 bytes
  * per 512-row block per head, rounded up to 256) and the fp16 scaled keys
- * (128 bytes per key, seq_len rounded up to 64, per head), then V^T when value
- * is head_dim-contiguous; 0 for a seq-contiguous value shorter than 4096 keys.
- * The pipelined launch (num_stages 3) uses only the V^T region. */
+ * (128 bytes per key, seq_len rounded up to 64, per head), then, for a
+ * seq-contiguous value, its key-major copy (128 bytes per key per head);
+ * 0 for a head_dim-contiguous value shorter than 4096 keys.  The pipelined
+ * launch (num_stages 3) uses at most the copy. */
 size_t sah_causal_attention_workspace_bytes(
     int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
     int64_t v_stride_s, int64_t v_stride_d, int dtype);
@@ -123,17 +125,18 @@ size_t sah_causal_attention_workspace_bytes(
  * workspace pair: the workspace is a static device array of
  * SAH_ATTENTION_STATIC_WORKSPACE_BYTES (64 MiB) that each GPU holds for the
  * life of the process.  From 4096 keys a call takes the prepared layout of
- * sah_causal_attention_bsd (norm tables, fp16 scaled keys, then V^T for a
- * head_dim-contiguous V) when it fits the array, with bitwise the same
+ * sah_causal_attention_bsd (norm tables, fp16 scaled keys, then the V copy
+ * for a seq-contiguous V) when it fits the array, with bitwise the same
  * result.  When it does not fit (for example BASELINE C4's B16 H32 S4096:
  * 268 MB of scaled keys), the call runs every workgroup on the plain kernel's
  * shifted path without the preparation launch, as below 4096 keys; that
- * needs only V^T for a head_dim-contiguous V (B*H*64*roundup(S, 64)*2 bytes)
- * and nothing for a seq-contiguous V, and its result agrees with
+ * needs nothing for a head_dim-contiguous V and only the key-major copy for
+ * a seq-contiguous V (B*H*S*64*2 bytes), and its result agrees with
  * sah_causal_attention_bsd's to the 16-bit tolerance, not bitwise.  The
- * pipelined launch (num_stages 3) needs only V^T.  A call whose V^T alone
- * exceeds the array returns SAH_ERR_WORKSPACE before any launch (B8 H16 S2048
- * fits; one 2 x 100000-token chunk with V in [B, H, S, 64] does not).  All
+ * pipelined launch (num_stages 3) needs at most the copy.  A call whose
+ * copy alone exceeds the array returns SAH_ERR_WORKSPACE before any launch
+ * (B8 H16 S2048 fits; one 2 x 100000-token chunk with a seq-contiguous V
+ * does not).  All
  * calls on one GPU share its array:
  * calls that may overlap on that GPU (different streams, or host threads)
  * race on it and must be serialized by the caller.  Nothing in it needs to
@@ -262,7 +265,7 @@ int sah_gelu_launch_supported(int block_size, int num_warps);
 typedef enum {
   SAH_QKV_VALUE_BHSD = 0,     /* [B, H, S, head_dim] contiguous, like query and key */
   SAH_QKV_VALUE_SEQ_MAJOR = 1 /* [B, H, head_dim, value_seq_stride]: seq-contiguous
-                                 (the V^T operand sah_causal_attention_bsd reads directly) */
+                                 (V^T; sah_causal_attention_bsd copies it key-major) */
 } sah_qkv_value_layout;
 
 /*
