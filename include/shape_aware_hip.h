@@ -124,20 +124,20 @@ size_t sah_causal_attention_workspace_bytes(
  * allocation.  Arguments are those of sah_causal_attention_bsd without the
  * workspace pair: the workspace is a static device array of
  * SAH_ATTENTION_STATIC_WORKSPACE_BYTES (64 MiB) that each GPU holds for the
- * life of the process.  From 4096 keys a call takes the prepared layout of
- * sah_causal_attention_bsd (norm tables, fp16 scaled keys, then the V copy
- * for a seq-contiguous V) when it fits the array, with bitwise the same
- * result.  When it does not fit (for example BASELINE C4's B16 H32 S4096:
- * 268 MB of scaled keys), the call runs every workgroup on the plain kernel's
- * shifted path without the preparation launch, as below 4096 keys; that
- * needs nothing for a head_dim-contiguous V and only the key-major copy for
- * a seq-contiguous V (B*H*S*64*2 bytes), and its result agrees with
- * sah_causal_attention_bsd's to the 16-bit tolerance, not bitwise.  The
- * pipelined launch (num_stages 3) needs at most the copy.  A call whose
- * copy alone exceeds the array returns SAH_ERR_WORKSPACE before any launch
- * (B8 H16 S2048 fits; one 2 x 100000-token chunk with a seq-contiguous V
- * does not).  All
- * calls on one GPU share its array:
+ * life of the process.  A call whose workspace (that of
+ * sah_causal_attention_bsd: norm tables and fp16 scaled keys from 4096 keys
+ * on, the key-major copy of a seq-contiguous V) fits the array runs as one
+ * call.  A larger one runs in chunks of heads of one batch row whose
+ * workspace fits (for example BASELINE C4's B16 H32 S4096, 268 MB of scaled
+ * keys: one call per batch row of 32 heads); heads are independent and each
+ * takes its path from its own tables, so the result is bitwise that of
+ * sah_causal_attention_bsd.  When even one head's prepared layout is above
+ * the array, every chunk runs the shifted path without the preparation
+ * launch, as below 4096 keys (equal to sah_causal_attention_bsd's result to
+ * the 16-bit tolerance, not bitwise).  A call for which one head's workspace
+ * still exceeds the array (a seq-contiguous V of more than 524288 keys)
+ * returns SAH_ERR_WORKSPACE before any launch.  All calls on one GPU share its
+ * array:
  * calls that may overlap on that GPU (different streams, or host threads)
  * race on it and must be serialized by the caller.  Nothing in it needs to
  * start at zero; every call writes what it reads.

@@ -1183,26 +1183,66 @@ extern "C" int sah_causal_attention_bsd_static_workspace(
     int64_t k_stride_s, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
     int64_t v_stride_d, int64_t o_stride_b, int64_t o_stride_s, float scale, int dtype,
     int block_m, int block_n, int num_warps, int num_stages, sah_stream_t stream) {
-  // The prepared layout when it fits the array; otherwise the plain kernel's
-  // shifted path for every workgroup, which needs at most the key-major copy
-  // of a seq-contiguous V^T.
+  // The whole call when its workspace fits the array.  Otherwise the call
+  // runs in chunks of heads of one batch row whose workspace fits: heads are
+  // independent and every head takes the same path (the path is chosen per
+  // head from its own tables), so the chunks give bitwise the result of one
+  // call.  The prepared layout is kept when one head's fits; otherwise every
+  // chunk runs the shifted path without preparation, as below 4096 keys.
   constexpr size_t kLimit = (size_t)SAH_ATTENTION_STATIC_WORKSPACE_BYTES;
-  const bool prepare = prepares(seq_len, num_stages, dtype) &&
-                       workspace_layout(batch, heads, seq_len, v_stride_d, dtype, true).total() <= kLimit;
-  const size_t need = workspace_layout(batch, heads, seq_len, v_stride_d, dtype, prepare).total();
-  if (need > kLimit)
-    return fail(SAH_ERR_WORKSPACE,
-                "attention needs %zu workspace bytes, above the static workspace of %zu bytes; "
-                "use sah_causal_attention_bsd with a caller-provided workspace",
-                need, kLimit);
+  const hipStream_t hip_stream = reinterpret_cast<hipStream_t>(stream);
+  bool prepare = prepares(seq_len, num_stages, dtype);
+  auto need_for = [&](int64_t b, int64_t h, bool prep) {
+    return workspace_layout(b, h, seq_len, v_stride_d, dtype, prep).total();
+  };
+  int64_t chunk_heads = heads;
+  const bool whole = need_for(batch, heads, prepare) <= kLimit;
+  if (!whole) {
+    if (prepare && need_for(1, 1, true) > kLimit) prepare = false;
+    // The most heads whose workspace fits (it grows with the head count).
+    int64_t lo = 0, hi = heads;
+    while (lo < hi) {
+      const int64_t mid = lo + (hi - lo + 1) / 2;
+      if (need_for(1, mid, prepare) <= kLimit)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    chunk_heads = lo;
+    if (chunk_heads == 0)
+      return fail(SAH_ERR_WORKSPACE,
+                  "attention needs %zu workspace bytes for one head, above the static workspace of "
+                  "%zu bytes; use sah_causal_attention_bsd with a caller-provided workspace",
+                  need_for(1, 1, prepare), kLimit);
+  }
+  const size_t need = need_for(whole ? batch : 1, chunk_heads, prepare);
   void* workspace = nullptr;
   if (need > 0) {
     workspace = scratch_address();
     if (workspace == nullptr) return SAH_ERR_HIP;
   }
-  return run_attention(query, key, value, output, batch, heads, seq_len, head_dim, q_stride_b,
-                       q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s, v_stride_b,
-                       v_stride_h, v_stride_s, v_stride_d, o_stride_b, o_stride_s, scale, dtype,
-                       block_m, block_n, num_warps, num_stages, workspace, need > 0 ? kLimit : 0,
-                       prepare, reinterpret_cast<hipStream_t>(stream));
+  if (whole)
+    return run_attention(query, key, value, output, batch, heads, seq_len, head_dim, q_stride_b,
+                         q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s, v_stride_b,
+                         v_stride_h, v_stride_s, v_stride_d, o_stride_b, o_stride_s, scale, dtype,
+                         block_m, block_n, num_warps, num_stages, workspace, need > 0 ? kLimit : 0,
+                         prepare, hip_stream);
+  // Element size of the 16-bit dtypes (fp32 calls need no workspace and
+  // never reach here).
+  const int64_t es = 2;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t h0 = 0; h0 < heads; h0 += chunk_heads) {
+      const int64_t hn = std::min(chunk_heads, heads - h0);
+      const char* q = static_cast<const char*>(query) + es * (b * q_stride_b + h0 * q_stride_h);
+      const char* k = static_cast<const char*>(key) + es * (b * k_stride_b + h0 * k_stride_h);
+      const char* v = static_cast<const char*>(value) + es * (b * v_stride_b + h0 * v_stride_h);
+      char* o = static_cast<char*>(output) + es * (b * o_stride_b + h0 * head_dim);
+      const int status = run_attention(
+          q, k, v, o, 1, hn, seq_len, head_dim, q_stride_b, q_stride_h, q_stride_s, k_stride_b,
+          k_stride_h, k_stride_s, v_stride_b, v_stride_h, v_stride_s, v_stride_d, o_stride_b,
+          o_stride_s, scale, dtype, block_m, block_n, num_warps, num_stages, workspace,
+          need > 0 ? kLimit : 0, prepare, hip_stream);
+      if (status != SAH_OK) return status;
+    }
+  return SAH_OK;
 }
