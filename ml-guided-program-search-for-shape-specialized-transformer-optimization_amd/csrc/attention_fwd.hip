@@ -1045,6 +1045,12 @@ int run_attention(
                 workspace_bytes);
   if (need > 0 && !aligned16(workspace))
     return fail(SAH_ERR_INVALID_ARGUMENT, "attention workspace must be 16-byte aligned");
+  // The preparation and V-copy launches put batch * heads on the grid's y axis.
+  if ((prepared || layout.vcopy > 0) && batch * heads > 65535)
+    return fail(SAH_ERR_UNSUPPORTED,
+                "attention with %s takes at most 65535 batch*heads (got %lld)",
+                prepared ? "the long-sequence preparation" : "a seq-contiguous value",
+                (long long)(batch * heads));
   const size_t norm_bytes = layout.norm;
   const size_t block_bytes = layout.block;
   const size_t kc_bytes = layout.kc;

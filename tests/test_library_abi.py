@@ -111,6 +111,16 @@ def test_invalid_arguments_fail_before_launch():
     for k_ss, v_ss in ((-64, 64), (1 << 24, 64), (64, 1 << 24), (64, -64)):
         assert attend(1000, k_ss, v_ss, 1) == _library.SAH_ERR_UNSUPPORTED, (k_ss, v_ss)
         assert b"32-bit tile offsets" in library.sah_last_error()
+    # The preparation and V-copy launches put batch * heads on the grid's y
+    # axis: more than 65535 is refused before any launch.
+    for seq, v_ss, v_sd in ((100, 1, 104), (5000, 64, 1)):
+        need = library.sah_causal_attention_workspace_bytes(65536, 1, seq, 64, v_ss, v_sd, 2)
+        assert need > 0
+        status = library.sah_causal_attention_bsd(
+            fake, fake, fake, fake, 65536, 1, seq, 64, 0, 0, 64, 0, 0, 64, 0, 0, v_ss, v_sd, 0, 64,
+            0.125, 2, 128, 64, 4, 2, fake, need, None)
+        assert status == _library.SAH_ERR_UNSUPPORTED, (seq, status)
+        assert b"65535 batch*heads" in library.sah_last_error()
     status = library.sah_residual_norm(
         fake, fake, None, None, fake, fake, 4, 1000, 1e-5, 2, 2, 2, 0, 0, 4, 4, None
     )
