@@ -149,6 +149,31 @@ def test_packed_qkv_view_and_transposed_value_layouts_agree(gpu_device):
     _assert_parity(reference, from_view, torch.bfloat16, "packed view")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("seq,launch", [(4500, (256, 8, 2)), (1000, (256, 8, 2)), (1000, (128, 4, 2)), (1000, (128, 4, 3))])
+def test_value_with_a_padded_key_stride_is_read_as_given(gpu_device, dtype, seq, launch):
+    """V head_dim-contiguous with a key stride of 72 elements, its rows padded
+    by 16 bytes that hold NaN: read as given (4500 keys: the scaled-key path's
+    direct-to-LDS ring with a partial last tile; 1000 keys: register-staged
+    tiles and the pipelined kernel), the PV operand transposed out of LDS.
+    Bitwise equal to the contiguous V, finite (the padding is never read) and
+    at parity with the oracle."""
+
+    print(f"padded V key stride dtype={dtype} S={seq} launch={launch}", flush=True)
+    q, k, v = _inputs(1, 3, seq, dtype=dtype, seed=seq + 7)
+    padded = torch.full((1, 3, seq, 72), float("nan"), dtype=dtype)
+    padded[..., :64] = v
+    v_padded = padded.to(gpu_device)[..., :64]
+    assert v_padded.stride(2) == 72 and v_padded.stride(3) == 1
+    block_m, warps, stages = launch
+    strided = _run(q, k, v_padded, gpu_device, block_m=block_m, num_warps=warps, num_stages=stages)
+    contiguous = _run(q, k, v, gpu_device, block_m=block_m, num_warps=warps, num_stages=stages)
+    assert bool(torch.isfinite(strided).all())
+    assert torch.equal(strided, contiguous)
+    reference = _to_bsd(_oracle(q, k, v, 1 / 8))
+    _assert_parity(reference, strided, dtype, f"padded V key stride S={seq} launch={launch}")
+
+
 @pytest.mark.parametrize("block_m,num_warps", [(256, 8), (512, 8), (128, 4)])
 def test_long_sequence_value_layouts_agree_with_poisoned_padding(gpu_device, block_m, num_warps):
     """S = 16500 (scaled-key path; the last key tile is partial, and so is its
