@@ -568,34 +568,38 @@ struct PrepParams {
   int heads, seq_len, key_tiles, num_row_blocks;
 };
 
-// Largest |row| of 64-row tile `tile` of a [S, 64] matrix with row stride
-// `ss` (squared, fp32, in every lane); with kc non-null the tile's rows times
-// c are written there in fp16.
+// Sum over the eight lanes of one row (lanes 8 r .. 8 r + 7) in every one of
+// them, by DPP moves: neighbour pairs, then pairs of pairs, then the mirrored
+// half-row, the order of a butterfly over lane bits 0, 1, 2 (each add is
+// commutative, so every lane holds the same bits).
+__device__ __forceinline__ float row8_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false)); // 7 - lane
+  return x;
+}
+
+// Sum of squares of the eight 16-bit values in `raw`, fp32, in element order.
 template <typename T>
-__device__ __forceinline__ float tile_max_sq(const T* base, int64_t ss, int tile, int seq_len,
-                                             f16* kc, float c, int lane) {
-  const int c8 = (lane & 7) * 8;
+__device__ __forceinline__ float chunk_sq(u32x4 raw) {
+  float f[8];
+  unpack8<T>(raw, f);
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf(f[e], f[e], s);
+  return s;
+}
+
+// Largest squared row norm of a 64-row tile held as raw[i] = 16 bytes of row
+// 8 i + lane / 8 (chunk lane % 8), rows at or past `valid` excluded; the
+// result is in every lane.
+template <typename T>
+__device__ __forceinline__ float tile_max_sq(const u32x4 (&raw)[8], int valid, int lane) {
   float mx = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int row = tile * 64 + 8 * i + (lane >> 3);
-    float ss2 = 0.0f;
-    if (row < seq_len) {
-      float f[8];
-      unpack8<T>(load16(base + (int64_t)row * ss + c8), f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss2 = fmaf(f[e], f[e], ss2);
-      if (kc != nullptr) {
-        f16x8 scaled;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) scaled[e] = (f16)fp32_result<f16>(f[e] * c);  // fp32 product, then fp16
-        store16(kc + (int64_t)row * kHeadDim + c8, __builtin_bit_cast(u32x4, scaled));
-      }
-    }
-    ss2 += __shfl_xor(ss2, 1);
-    ss2 += __shfl_xor(ss2, 2);
-    ss2 += __shfl_xor(ss2, 4);
-    mx = fmaxf(mx, ss2);
+    const float ss2 = row8_sum(chunk_sq<T>(raw[i]));
+    if (8 * i + (lane >> 3) < valid) mx = fmaxf(mx, ss2);
   }
 #pragma unroll
   for (int offset = 32; offset >= 8; offset >>= 1) mx = fmaxf(mx, __shfl_xor(mx, offset));
@@ -615,21 +619,58 @@ __global__ __launch_bounds__(256) void long_prepare_kernel(PrepParams pp) {
   constexpr int kTilesPerBlock = kScaledKeyRows / 64;
   const int t0 = blk * kTilesPerBlock;
   const int t_end = min(t0 + kTilesPerBlock, pp.key_tiles);
+  const int S = pp.seq_len;
 
   const T* kbase = static_cast<const T*>(pp.k) + b * pp.k_sb + h * pp.k_sh;
   const T* qbase = static_cast<const T*>(pp.q) + b * pp.q_sb + h * pp.q_sh;
   f16* kc = pp.kc + (int64_t)bh * pp.key_tiles * 64 * kHeadDim;
+  const int c8 = (lane & 7) * 8;
+
+  // Every load of the wave's two K tiles and two Q tiles is issued before
+  // any is used: rows past the sequence (and tiles past the block's end)
+  // read row S - 1 instead, and are left out of the maxima and the stores.
+  u32x4 kraw[2][8], qraw[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min((t0 + 2 * wave + j) * 64 + 8 * i + (lane >> 3), S - 1);
+      kraw[j][i] = load16(kbase + (int64_t)row * pp.k_ss + c8);
+    }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = min((t0 + 2 * wave + j) * 64 + 8 * i + (lane >> 3), S - 1);
+      qraw[j][i] = load16(qbase + (int64_t)row * pp.q_ss + c8);
+    }
+
+  // A tile past the block's end lies past the sequence (t_end < t0 + 8 only
+  // for the last block), so it has no valid rows: it adds 0 to the maxima and
+  // writes nothing.
   float kmax = 0.0f, qmax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int t = t0 + 2 * wave + i;
-    if (t < t_end) {  // wave-uniform
-      const float km = tile_max_sq<T>(kbase, pp.k_ss, t, pp.seq_len, kc, pp.c, lane);
-      const float qm = tile_max_sq<T>(qbase, pp.q_ss, t, pp.seq_len, nullptr, 0.0f, lane);
-      if (lane == 0) pp.knorm[(int64_t)bh * pp.key_tiles + t] = sqrtf(km);
-      kmax = fmaxf(kmax, km);
-      qmax = fmaxf(qmax, qm);
+  for (int j = 0; j < 2; ++j) {
+    const int t = t0 + 2 * wave + j;
+    const int valid = S - t * 64;  // rows of the tile inside the sequence
+    // Keys times c, rounded once to fp16 (fp32 product, then fp16).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      if (r < valid) {
+        float f[8];
+        unpack8<T>(kraw[j][i], f);
+        f16x8 scaled;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) scaled[e] = (f16)fp32_result<f16>(f[e] * pp.c);
+        store16(kc + (int64_t)(t * 64 + r) * kHeadDim + c8, __builtin_bit_cast(u32x4, scaled));
+      }
     }
+    const float km = tile_max_sq<T>(kraw[j], valid, lane);
+    const float qm = tile_max_sq<T>(qraw[j], valid, lane);
+    if (lane == 0 && t < t_end) pp.knorm[(int64_t)bh * pp.key_tiles + t] = sqrtf(km);
+    kmax = fmaxf(kmax, km);
+    qmax = fmaxf(qmax, qm);
   }
   if (lane == 0) {
     red[0][wave] = kmax;
@@ -642,7 +683,6 @@ __global__ __launch_bounds__(256) void long_prepare_kernel(PrepParams pp) {
     pp.kblock[(int64_t)bh * pp.num_row_blocks + blk] = sqrtf(k4);
     pp.qblock[(int64_t)bh * pp.num_row_blocks + blk] = pp.zero_q ? 0.0f : sqrtf(q4);
   }
-
 }
 
 // A seq-contiguous V^T [B, H, 64, >=S] (seq stride 1, head_dim stride
