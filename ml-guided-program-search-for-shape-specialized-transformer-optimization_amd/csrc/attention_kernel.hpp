@@ -549,7 +549,10 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
       for (int r = 0; r < 16; ++r) acc[g][d][r] = 0.0f;
   }
   const float c = p.c;
-  const bool bounded = p.knorm != nullptr;  // uniform
+  // The key-norm table exists only with the preparation pass, whose blocks
+  // run kPathScaled or kPathShifted; the host sets knorm and kc together, so
+  // a kPathAll launch never has it and drops the per-tile bound check.
+  const bool bounded = PATH != kPathAll && p.knorm != nullptr;  // uniform
   // Global address space spelled out: the table entry of the next tile is
   // then a scalar load (uniform address, read-only).  Left to inference the
   // compiler emitted a flat load here, whose completion every later LDS wait
