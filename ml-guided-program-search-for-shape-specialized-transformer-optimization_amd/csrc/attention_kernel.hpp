@@ -275,9 +275,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // query row.  v_permlane32_swap exchanges the halves of two registers; the max
 // (or sum) of the two results is the cross-half value in every lane, whichever
 // half each register received.
+// The max is one v_max_f32 written as assembly: through fmaxf the compiler
+// first quiets both swapped values (two more v_max_f32), since it cannot see
+// that a lane move keeps them canonical.
 __device__ __forceinline__ float half_swap_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
 }
 __device__ __forceinline__ float half_swap_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -696,7 +701,9 @@ __global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES,
             // results do not depend on the launch.
             const bool need = !bounded || qnc[g] * kn - m_run[g] * c > safe_exponent<T>();
             if (__any(need)) {
-              float mx = sacc[g][0][0];
+              // From -inf the chain compiles to v_max3 only (starting from an
+              // element, the compiler quiets the first two operands first).
+              float mx = -INFINITY;
 #pragma unroll
               for (int t = 0; t < 2; ++t)
 #pragma unroll
