@@ -18,7 +18,6 @@ Two references:
 
 from __future__ import annotations
 
-import ctypes
 
 import pytest
 import torch

@@ -11,7 +11,6 @@ activation or a transposed operand would far exceed.
 
 from __future__ import annotations
 
-import ctypes
 
 import pytest
 import torch

@@ -19,7 +19,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from oracle.compare import model_parity, official_compare, parity_gate
+from oracle.compare import model_parity, parity_gate
 from oracle.forward import TransformerConfig, cast_state, forward, generate_input, xavier_init_weights
 
 pytestmark = pytest.mark.gpu

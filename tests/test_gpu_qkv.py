@@ -14,7 +14,6 @@ both by far.
 
 from __future__ import annotations
 
-import ctypes
 
 import pytest
 import torch

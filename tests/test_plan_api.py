@@ -24,7 +24,6 @@ from solution.config import (
     TritonAttentionParams,
     hip_config,
     portable_config,
-    portable_streamed_config,
 )
 from solution.plan import ExecutionContext
 from solution.plan_builder import ConfigRejectedError, HardwareCapabilities, PlanBuilder
