@@ -57,6 +57,8 @@ with its projection: the fused HIP Linear + residual + LayerNorm kernel, or
 hipBLASLt F.linear followed by the HIP residual LayerNorm, for the attention
 output projection (D -> D) or the FFN output projection (F -> D).  Attention runs with
 the long-sequence program's launch (HIP_LONG_SEQUENCE_ATTENTION_LAUNCH).
+``--kernel attention-c4`` runs BASELINE configs[3]'s attention alone (B16 H32
+S4096 from the packed QKV view, launch 256/64/8/2) for counter runs.
 
 ``config3`` in the JSON line reports BASELINE.json's operator-alone
 configuration, timed before the forward on the idle GPU: the attention op
@@ -562,6 +564,18 @@ def kernel_alone(kind: str, repeat: int, data: str = "random") -> int:
             run = lambda: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
                 q, k, v, scale=scale, block_m=launch.block_m, block_n=launch.block_n,
                 num_warps=launch.num_warps, num_stages=launch.num_stages)
+            work = f"{_attention_flops(q) / 1e12:.3f} TFLOP per launch"
+        elif kind == "attention-c4":
+            # BASELINE configs[3]'s attention, B16 H32 S4096, from the packed
+            # QKV view the resident program hands over, with its registry
+            # launch (256/64/8/2, preparation and scaled-key path).
+            c4_batch, c4_seq, c4_width, c4_heads = RESIDENT_SHAPES["c4"][:4]
+            packed = torch.randn(c4_batch, c4_seq, 3 * c4_width, generator=generator, device=device,
+                                 dtype=torch.bfloat16)
+            q, k, v = (t.transpose(1, 2) for t in packed.unflatten(-1, (3, c4_heads, c4_width // c4_heads)).unbind(dim=2))
+            scale = 1.0 / math.sqrt(c4_width // c4_heads)
+            run = lambda: hip_streaming_dh64.hip_streaming_dh64_causal_attention_bsd(
+                q, k, v, scale=scale, block_m=256, block_n=64, num_warps=8, num_stages=2)
             work = f"{_attention_flops(q) / 1e12:.3f} TFLOP per launch"
         elif kind == "norm":
             value = torch.randn(batch * seq, width, generator=generator, device=device, dtype=torch.bfloat16)
@@ -1078,7 +1092,7 @@ def main() -> int:
                         help="skip the operator-alone figures (e.g. for a kernel trace of the forward alone)")
     parser.add_argument("--kernel", choices=("attention", "norm", "copy", "linear", "linear-torch", "gelu", "gelu-torch",
                                              "qkv", "qkv-torch", "boundary", "boundary-torch", "boundary-ffn",
-                                             "boundary-ffn-torch", "attention-c3", "norm-c3"),
+                                             "boundary-ffn-torch", "attention-c3", "norm-c3", "attention-c4"),
                         help="run one kernel alone at the per-chunk shape (profiling)")
     parser.add_argument("--repeat", type=int, default=3, help="launches for --kernel")
     parser.add_argument("--launch", type=lambda text: tuple(int(x) for x in text.split(",")),
