@@ -289,15 +289,6 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// The double-buffered 8-wave, 32-rows-per-wave instantiations (the
-// long-sequence launch) must keep 4 wavefronts per SIMD (<= 128 VGPRs): the
-// second bound is the minimum wavefronts per SIMD.  The single-buffered twins
-// would spill under it and are left unbounded.
-template <typename T, int QG, int STAGES, int WAVES>
-constexpr int attn_min_waves_per_simd() {
-  return (QG == 1 && WAVES == 8 && STAGES == 2) ? 4 : 1;
-}
-
 // PATH: kPathAll runs every workgroup on the shifted path (no scaled keys);
 // with the scaled keys, kPathScaled runs the workgroups that qualify for the
 // scaled-key path and kPathShifted the others, as two launches over the same
@@ -307,8 +298,19 @@ constexpr int kPathAll = 0;
 constexpr int kPathScaled = 1;
 constexpr int kPathShifted = 2;
 
+// Wavefronts per SIMD the kernel must keep (the second __launch_bounds__
+// argument; 4 waves per SIMD means <= 128 VGPRs): the double-buffered 8-wave,
+// 32-rows-per-wave instantiations (the long-sequence launch), and the 4-wave,
+// 32-rows-per-wave instantiations of the shifted paths (128-row tiles; four
+// workgroups per CU instead of three).  Their scaled-key twins and the
+// single-buffered 8-wave ones would spill under it and are left unbounded.
 template <typename T, int QG, int STAGES, int WAVES, int PATH>
-__global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES, WAVES>())) void attn_fwd_kernel(AttnParams p) {
+constexpr int attn_min_waves_per_simd() {
+  return (QG == 1 && ((WAVES == 8 && STAGES == 2) || (WAVES == 4 && PATH != kPathScaled))) ? 4 : 1;
+}
+
+template <typename T, int QG, int STAGES, int WAVES, int PATH>
+__global__ __launch_bounds__(WAVES * 64, (attn_min_waves_per_simd<T, QG, STAGES, WAVES, PATH>())) void attn_fwd_kernel(AttnParams p) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec8<T>::half_type V4;
   typedef typename Vec8<T>::pair_type V2;
